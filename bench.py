@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Attention-forward benchmark on one MI355X.
+
+Workload (default ``c3``): the Llama-3-8B-shaped GQA causal config of
+BASELINE.json -- B=1, S=8192, 32 query / 8 KV heads, D=128, bf16, RoPE base
+5e5 on q and k.  One "step" = one ``triton_attn_func`` call on resident
+inputs with the RoPE fused (q rotated inside the attention kernel, k by the
+RoPE pre-pass kernel).
+
+Printed as ONE JSON line:
+  value        algorithmic TFLOP/s of the whole step (4*D*allowed pairs;
+               masked pairs not counted) / measured step time;
+  roofline     for the attention kernel alone: algorithmic flops per launch
+               / its mean launch time (HIP events on the launch stream),
+               against the dense bf16 MFMA peak of MI355X (2.5 PFLOP/s);
+  cpu_baseline the CPU oracle (restated reference eager path) on a bounded
+               sample of the same workload, on this host's cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "attn fwd TFLOP/s + % of MI355X bf16 MFMA peak (1 GPU); vs CPU ref ms"
+PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
+DTYPE_NAME = {"torch.bfloat16": "bf16", "torch.float16": "fp16", "torch.float32": "fp32"}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="c3")
+    ap.add_argument("--cpu-sample-heads", type=int, default=4,
+                    help="query heads of batch 0 timed on the CPU oracle")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--all", action="store_true", help="also time every other workload (extra field)")
+    return ap.parse_args()
+
+
+def step_fn(w, inp, torch):
+    from trinix_amd import triton_attn_func
+
+    kw = dict(causal=w.causal)
+    if w.window is not None:
+        kw["window_size"] = w.window
+    if inp.mask is not None:
+        kw["attn_mask"] = inp.mask
+    if inp.alibi is not None:
+        kw["alibi_slopes"] = inp.alibi
+    if inp.cos is not None:
+        kw["rotary_cos"], kw["rotary_sin"] = inp.cos, inp.sin
+    k, v = inp.k, inp.v
+    if w.nheads_kv == 1:  # MQA: one KV head, expanded with stride 0 as the reference layer does
+        k = k.expand(-1, -1, w.nheads, -1)
+        v = v.expand(-1, -1, w.nheads, -1)
+    return lambda: triton_attn_func(inp.q, k, v, **kw)
+
+
+def kernel_only_fn(w, inp, torch):
+    """The attention kernel alone: k pre-rotated once, q rotated in-kernel."""
+    from trinix_amd.kernels import TritonAttentionKernel, rope_apply
+
+    k, v = inp.k, inp.v
+    kw = dict(causal=w.causal, window_size=w.window, attn_mask=inp.mask, alibi_slopes=inp.alibi)
+    if inp.cos is not None:
+        k = rope_apply(inp.k, inp.cos, inp.sin)
+        kw.update(rotary_cos=inp.cos, rotary_sin=inp.sin, rotary_k=False)
+    if w.nheads_kv == 1:
+        k = k.expand(-1, -1, w.nheads, -1)
+        v = v.expand(-1, -1, w.nheads, -1)
+    return lambda: TritonAttentionKernel.apply(inp.q, k, v, **kw)
+
+
+def time_events(fn, iters, torch):
+    """Mean ms per call from HIP events on the current (launch) stream."""
+    st = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(st)
+    for _ in range(iters):
+        fn()
+    end.record(st)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def measure(w, args, torch):
+    from trinix_amd.workloads import make_inputs, flops
+
+    inp = make_inputs(w, device="cuda")
+    fn = step_fn(w, inp, torch)
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fn()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    fl = flops(w)
+    kfn = kernel_only_fn(w, inp, torch)
+    for _ in range(2):
+        kfn()
+    kms = time_events(kfn, max(args.steps, 10), torch)
+    return inp, fl, ms, kms
+
+
+def cpu_baseline(w, nheads, torch):
+    """Oracle (restated reference eager path) on `nheads` query heads of
+    batch 0, RoPE applied outside the timed region; 1 warm-up + median of 3
+    (1 run if the sample takes > 20 s)."""
+    from oracle.attention_oracle import apply_rope, functional_attention
+    from trinix_amd.workloads import make_inputs, flops
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    inp = make_inputs(w)
+    q, k = inp.q, inp.k
+    if inp.cos is not None:
+        q, k = apply_rope(q, inp.cos, inp.sin), apply_rope(k, inp.cos, inp.sin)
+    heads = list(range(min(nheads, w.nheads)))
+    kw = dict(attn_mask=inp.mask, causal=w.causal, window_size=w.window, alibi_slopes=inp.alibi,
+              heads=heads, batches=[0])
+    t0 = time.perf_counter()
+    functional_attention(q, k, inp.v, **kw)
+    first = time.perf_counter() - t0
+    times = [first]
+    if first < 20:
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            functional_attention(q, k, inp.v, **kw)
+            times.append(time.perf_counter() - t0)
+    t = sorted(times)[len(times) // 2]
+    fl = flops(w, heads=heads, batches=[0])
+    full_ms = t * 1e3 * (w.batch * w.nheads) / len(heads)
+    return {
+        "value": round(fl / t / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{len(heads)} of {w.batch * w.nheads} (batch, q-head) slices of {w.name}, "
+                  f"eager bmm/softmax path in {DTYPE_NAME[str(w.dtype)]}, median of {len(times)}",
+        "sample_ms": round(t * 1e3, 2),
+        "full_config_ms_extrapolated": round(full_ms, 1),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); "
+              "this build has no multi-GPU path", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from trinix_amd.workloads import WORKLOADS
+    from trinix_amd import _native
+
+    w = WORKLOADS[args.workload]
+    dname = DTYPE_NAME[str(w.dtype)]
+    inp, fl, ms, kms = measure(w, args, torch)
+    value = fl / (ms * 1e-3) / 1e12
+    k_tflops = fl / (kms * 1e-3) / 1e12
+    peak = PEAK_TFLOPS[dname]
+    rec = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": dname,
+        "data": "synthetic (seeded N(0,1) q/k/v)",
+        "config": {
+            "workload": f"{w.name}: {w.description}",
+            "batch": w.batch, "seq_len": w.seqlen, "nheads_q": w.nheads, "nheads_kv": w.nheads_kv,
+            "head_dim": w.head_dim, "causal": w.causal, "window": w.window, "rope_base": w.rope_base,
+            "alibi": w.alibi, "block_mask": w.block_mask, "fused_rope": w.rope_base is not None,
+            "algorithmic_flop": fl, "parallelism": "single GPU",
+        },
+        "pct_of_peak": round(100 * value / peak, 2),
+        "roofline": {
+            "bound": "mfma",
+            "kernel": "attn_fwd_mfma16" if dname != "fp32" else "attn_fwd_f32",
+            "achieved": round(k_tflops, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(k_tflops / peak, 4),
+            "kernel_ms": round(kms, 4),
+            "traffic": None,
+        },
+        "native_library": str(_native.LIB_PATH) if _native.library_loaded() else None,
+    }
+    if args.all:
+        extra = {}
+        for name, wo in WORKLOADS.items():
+            if name == w.name:
+                continue
+            _, f2, ms2, kms2 = measure(wo, args, torch)
+            pk = PEAK_TFLOPS[DTYPE_NAME[str(wo.dtype)]]
+            extra[name] = {"ms": round(ms2, 4), "tflops": round(f2 / ms2 / 1e9, 2),
+                           "kernel_ms": round(kms2, 4), "kernel_tflops": round(f2 / kms2 / 1e9, 2),
+                           "pct_of_peak": round(100 * f2 / ms2 / 1e9 / pk, 2)}
+            torch.cuda.empty_cache()
+        rec["other_workloads"] = extra
+    if not args.no_cpu:
+        del inp
+        torch.cuda.empty_cache()
+        rec["cpu_baseline"] = cpu_baseline(w, args.cpu_sample_heads, torch)
+        rec["speedup_vs_cpu_full_config"] = round(rec["cpu_baseline"]["full_config_ms_extrapolated"] / ms, 1)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,157 @@
+/*
+ * trinix_attn.h -- C ABI of the MI355X (gfx950) attention-forward library
+ * `libtrinix_attn.so`.
+ *
+ * Plain C: pointers, sizes and strides only, no torch or HIP types in the
+ * signatures (streams travel as `void*`, a `hipStream_t`; NULL = the null
+ * stream).  Every entry point is asynchronous on the given stream, allocates
+ * no device memory, frees nothing, and returns a `trinix_status` code; no C++
+ * exception crosses the boundary.  Tensors are owned by the caller.
+ *
+ * Strides are in ELEMENTS, in the reference's BSHD order
+ * (batch, seq, head, head_dim) for q/k/v/out; the head_dim stride must be 1.
+ * A head stride of 0 on k/v (an `expand`ed single KV head) is accepted.
+ *
+ * Reference interfaces replaced (paths relative to the trinix 0.1.4 tree):
+ *   trinix_attn_fwd            <- TritonAttentionKernel.apply
+ *                                 trinix/kernels/attention_kernel.py:497-664
+ *                                 (launch of _fwd_kernel :234-434 and
+ *                                 _fwd_kernel_with_mask :8-231)
+ *   trinix_attn_mask_blockmap  <- TritonAttentionKernel._prepare_mask
+ *                                 trinix/kernels/attention_kernel.py:479-495
+ *                                 (the (B,H,S,S) materialisation is replaced
+ *                                 by a per-block classification of the mask)
+ *   trinix_rope_apply          <- TritonRoPEKernel.apply / _apply_rope_pytorch
+ *                                 trinix/kernels/rope_kernel.py:180-222,
+ *                                 trinix/layers/embeddings/rope.py:111-134
+ *   trinix_attn_tile_config    <- calculate_attention_block_sizes
+ *                                 trinix/kernels/utils.py:87-153
+ *   trinix_attn_is_available   <- TritonAttentionKernel.is_available
+ *                                 trinix/kernels/attention_kernel.py:470-477
+ */
+#ifndef TRINIX_ATTN_H
+#define TRINIX_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRINIX_ATTN_ABI_VERSION 1
+
+typedef enum trinix_status {
+  TRINIX_OK = 0,
+  TRINIX_ERR_NULL_POINTER = 1,   /* a required pointer is NULL             */
+  TRINIX_ERR_BAD_DTYPE = 2,      /* unsupported dtype / dtype mismatch      */
+  TRINIX_ERR_BAD_HEAD_DIM = 3,   /* head_dim not in {64, 128}               */
+  TRINIX_ERR_BAD_SHAPE = 4,      /* non-positive or inconsistent sizes      */
+  TRINIX_ERR_BAD_STRIDE = 5,     /* d-stride != 1 or misaligned rows        */
+  TRINIX_ERR_BAD_ARGUMENT = 6,   /* other invalid argument (dropout, ...)   */
+  TRINIX_ERR_NO_DEVICE = 7,      /* no gfx950 device / HIP runtime error    */
+  TRINIX_ERR_LAUNCH = 8          /* hipGetLastError after the launch        */
+} trinix_status;
+
+typedef enum trinix_dtype {
+  TRINIX_F32 = 0,
+  TRINIX_F16 = 1,
+  TRINIX_BF16 = 2,
+  TRINIX_U8 = 3 /* bool / uint8 masks only: value 0 or 1 is added */
+} trinix_dtype;
+
+/* Arguments of one attention forward.  Semantics (reference
+ * trinix/kernels/attention_kernel.py:123-216):
+ *   s[i,j] = scale * <q[b,i,hq], k[b,j,hkv]>
+ *            - alibi[b,hq] * |i - j|          (if alibi_slopes)
+ *            + mask[b,hq,i,j]                 (if mask)
+ *   s[i,j] = -inf unless  j < seqlen_k,
+ *                         j <= i              (if causal; top-left aligned),
+ *                         -wl <= j - i <= wr  (if has_window)
+ *   out[b,i,hq,:] = softmax_j(s[i,:]) @ v[b,:,hkv,:]
+ *   hkv = hq / (nheads_q / nheads_kv)   (GQA/MQA without repeating KV)
+ *   lse[b,hq,i] = log(sum_j exp(s[i,j]))  (natural log; optional)
+ * Rows with no allowed key give NaN, as softmax over all -inf does.
+ */
+typedef struct trinix_attn_fwd_args {
+  const void* q;        /* (B, Sq, Hq, D)  */
+  const void* k;        /* (B, Sk, Hkv, D) */
+  const void* v;        /* (B, Sk, Hkv, D) */
+  void* out;            /* (B, Sq, Hq, D), dtype of q */
+  float* lse;           /* (B, Hq, Sq) fp32 contiguous, or NULL */
+  int64_t q_stride[4];  /* b, s, h, d */
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t out_stride[4];
+  int64_t batch, seqlen_q, seqlen_k, nheads_q, nheads_kv, head_dim;
+  int32_t dtype;        /* trinix_dtype of q, k, v, out */
+  float softmax_scale;
+  int32_t causal;
+  int32_t has_window;
+  int64_t window_left, window_right;
+  const float* alibi_slopes;    /* fp32, element (b, h) at b*s[0] + h*s[1]; NULL = none */
+  int64_t alibi_stride[2];
+  const void* mask;             /* additive mask, NULL = none */
+  int32_t mask_dtype;           /* trinix_dtype */
+  int64_t mask_stride[4];       /* b, h, i, j (0 = broadcast) */
+  const uint8_t* mask_blockmap; /* from trinix_attn_mask_blockmap, or NULL */
+  int64_t blockmap_stride[2];   /* b, h strides of the block map (0 = broadcast) */
+  float dropout_p;              /* 0 <= p < 1 */
+  uint64_t dropout_seed;
+  uint64_t dropout_offset;
+  const void* rope_cos;         /* fused RoPE on q: cos/sin rows indexed by the  */
+  const void* rope_sin;         /* query position, first D/2 columns used; dtype */
+  int64_t rope_stride;          /* of q; NULL = no fused RoPE                    */
+} trinix_attn_fwd_args;
+
+/* Attention forward on `stream`. */
+int trinix_attn_fwd(const trinix_attn_fwd_args* args, void* stream);
+
+/* Block classification of an additive mask of logical size
+ * (mb, mh, seqlen_q, seqlen_k) with element strides `stride` (0 = broadcast).
+ * Writes out[((b*mh + h)*ceil(Sq/32) + r)*ceil(Sk/64) + c] for each 32x64
+ * block: 0 = every element is +0/-0 (no load needed), 2 = every element is
+ * -inf (block skipped), 1 = anything else (loaded per element). */
+int trinix_attn_mask_blockmap(const void* mask, int32_t mask_dtype,
+                              int64_t mb, int64_t mh, int64_t seqlen_q,
+                              int64_t seqlen_k, const int64_t stride[4],
+                              uint8_t* out, void* stream);
+/* Rows and columns covered by one block-map entry. */
+#define TRINIX_BLOCKMAP_ROWS 32
+#define TRINIX_BLOCKMAP_COLS 64
+
+/* Rotary embedding, reference trinix/layers/embeddings/rope.py:111-134:
+ *   out = x*cos + rotate_half(x)*sin, rotate_half(x) = cat(-x2, x1),
+ * with every product and the sum rounded to the tensor dtype, as eager
+ * PyTorch does.  x, out: (B, S, H, D) with strides (d stride 1); cos/sin:
+ * rows of >= D/2 entries in x's dtype with row stride `cs_stride`; row
+ * index = position_ids[b*S + s] (int64) if position_ids != NULL, else s. */
+int trinix_rope_apply(const void* x, const int64_t x_stride[4], void* out,
+                      const int64_t out_stride[4], int64_t batch,
+                      int64_t seqlen, int64_t nheads, int64_t head_dim,
+                      int32_t dtype, const void* cos, const void* sin,
+                      int64_t cs_stride, const int64_t* position_ids,
+                      void* stream);
+
+/* Tile shape the library launches for (head_dim, dtype). */
+typedef struct trinix_tile_cfg {
+  int32_t block_m;      /* query rows per workgroup     */
+  int32_t block_n;      /* keys per K/V tile            */
+  int32_t block_d;      /* head_dim the kernel runs at  */
+  int32_t waves;        /* wavefronts per workgroup     */
+  int32_t lds_bytes;    /* LDS per workgroup            */
+} trinix_tile_cfg;
+int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* out);
+
+/* 1 if a gfx950 device is visible to the HIP runtime, else 0. */
+int trinix_attn_is_available(void);
+
+/* Static description of a status code. */
+const char* trinix_status_string(int status);
+
+/* TRINIX_ATTN_ABI_VERSION of the built library. */
+int trinix_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TRINIX_ATTN_H */

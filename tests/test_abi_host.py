@@ -1,0 +1,132 @@
+"""CPU-only checks of the C ABI library and the host logic: the library
+loads, exports every function ``include/trinix_attn.h`` declares, the ctypes
+mirror of ``trinix_attn_fwd_args`` has the C layout, argument validation
+returns the right status codes (no kernel is launched), and the Python layer
+raises the reference's exception types."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+import torch
+
+from trinix_amd import _native as nat
+from trinix_amd.build import LIB_PATH, INCLUDE_DIR, build
+
+HEADER = os.path.join(INCLUDE_DIR, "trinix_attn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB_PATH.exists():
+        build()
+    return nat.load_library()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(trinix_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 7
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(nat.SIGNATURES), "ctypes signature table out of sync with the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(LIB_PATH)], capture_output=True, text=True).stdout
+    for n in names:
+        assert re.search(rf"\bT {n}$", out, re.M), n
+
+
+def test_struct_layout_matches_c(lib):
+    fields = [f for f, _ in nat.AttnFwdArgs._fields_]
+    prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "trinix_attn.h"', "int main(void){",
+            'printf("%zu\\n", sizeof(trinix_attn_fwd_args));']
+    prog += [f'printf("%zu\\n", offsetof(trinix_attn_fwd_args, {f}));' for f in fields]
+    prog += ['printf("%zu\\n", sizeof(trinix_tile_cfg));', "return 0;}"]
+    with tempfile.TemporaryDirectory() as d:
+        src, exe = os.path.join(d, "l.c"), os.path.join(d, "l")
+        open(src, "w").write("\n".join(prog))
+        subprocess.run(["gcc", "-std=c99", "-I", str(INCLUDE_DIR), src, "-o", exe], check=True)
+        vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
+    assert vals[0] == ctypes.sizeof(nat.AttnFwdArgs)
+    for f, off in zip(fields, vals[1:-1]):
+        assert getattr(nat.AttnFwdArgs, f).offset == off, f
+    assert vals[-1] == ctypes.sizeof(nat.TileCfg)
+
+
+def test_version_status_and_tiles(lib):
+    assert lib.trinix_abi_version() == nat.ABI_VERSION
+    for code in range(9):
+        assert lib.trinix_status_string(code)
+    cfg = nat.TileCfg()
+    assert lib.trinix_attn_tile_config(128, nat.TRINIX_BF16, ctypes.byref(cfg)) == 0
+    assert cfg.block_d == 128 and cfg.block_m % 32 == 0 and cfg.block_n % 64 == 0
+    assert lib.trinix_attn_tile_config(96, nat.TRINIX_BF16, ctypes.byref(cfg)) == nat.TRINIX_ERR_BAD_HEAD_DIM
+    assert lib.trinix_attn_tile_config(64, 9, ctypes.byref(cfg)) == nat.TRINIX_ERR_BAD_DTYPE
+
+
+def _args(**kw):
+    a = nat.AttnFwdArgs()
+    a.q = a.k = a.v = a.out = 4096
+    for name in ("q_stride", "k_stride", "v_stride", "out_stride"):
+        setattr(a, name, nat.int64x4((8 * 64 * 128, 8 * 128, 128, 1)))
+    a.batch, a.seqlen_q, a.seqlen_k, a.nheads_q, a.nheads_kv, a.head_dim = 1, 64, 64, 8, 8, 128
+    a.dtype = nat.TRINIX_BF16
+    a.softmax_scale = 0.1
+    for k_, v_ in kw.items():
+        setattr(a, k_, v_)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(head_dim=96), nat.TRINIX_ERR_BAD_HEAD_DIM),
+    (dict(dtype=7), nat.TRINIX_ERR_BAD_DTYPE),
+    (dict(nheads_kv=3), nat.TRINIX_ERR_BAD_SHAPE),
+    (dict(seqlen_q=0), nat.TRINIX_ERR_BAD_SHAPE),
+    (dict(q=None), nat.TRINIX_ERR_NULL_POINTER),
+    (dict(q_stride=nat.int64x4((1, 1, 1, 2))), nat.TRINIX_ERR_BAD_STRIDE),
+    (dict(k_stride=nat.int64x4((8 * 64 * 128, 8 * 128, 130, 1))), nat.TRINIX_ERR_BAD_STRIDE),
+    (dict(dropout_p=1.0), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(mask_blockmap=4096), nat.TRINIX_ERR_BAD_ARGUMENT),
+])
+def test_validation_rejects_before_launch(lib, kw, code):
+    a = _args(**kw)
+    assert lib.trinix_attn_fwd(ctypes.byref(a), None) == code
+
+
+def test_status_to_exception_types(lib):
+    with pytest.raises(ValueError):
+        nat.check(nat.TRINIX_ERR_BAD_SHAPE, "x")
+    with pytest.raises(RuntimeError):
+        nat.check(nat.TRINIX_ERR_LAUNCH, "x")
+    nat.check(nat.TRINIX_OK, "x")
+
+
+def test_functional_api_errors_match_reference():
+    from trinix_amd import triton_attn_func
+    from trinix_amd.kernels import TritonAttentionKernel
+
+    q = torch.zeros(1, 4, 2, 64)
+    with pytest.raises(ValueError, match="only supports CUDA tensors"):
+        triton_attn_func(q, q, q)
+    m4 = TritonAttentionKernel._prepare_mask(torch.zeros(4, 4), 2, 3, 4)
+    assert m4.shape == (2, 3, 4, 4) and m4.stride()[:2] == (0, 0)
+    m4 = TritonAttentionKernel._prepare_mask(torch.zeros(2, 4, 4), 2, 3, 4)
+    assert m4.stride(1) == 0 and m4.stride(0) == 16
+    m4 = TritonAttentionKernel._prepare_mask(torch.zeros(2, 1, 4, 6), 2, 3, 4, 6)
+    assert m4.shape == (2, 3, 4, 6)
+    with pytest.raises(ValueError, match="Unsupported mask shape"):
+        TritonAttentionKernel._prepare_mask(torch.zeros(1, 1, 1, 4, 4), 1, 1, 4)
+    with pytest.raises(ValueError):
+        TritonAttentionKernel._prepare_mask(torch.zeros(5, 4), 1, 1, 4)
+    assert not TritonAttentionKernel.is_available()  # no GPU in this process
+
+
+def test_kernel_head_dim_padding_rule():
+    from trinix_amd.kernels.attention_kernel import kernel_head_dim
+
+    assert [kernel_head_dim(d) for d in (8, 32, 64, 65, 80, 128, 129)] == [64, 64, 64, 128, 128, 128, None]

@@ -1,0 +1,341 @@
+"""GPU parity tests: the HIP attention path (through the C ABI) against the
+CPU oracle (a restatement of the reference eager path) on identical seeded
+inputs.
+
+Tolerances (stated by the north star): bf16/fp16 outputs max abs <= 2e-2
+and mean abs <= 2e-3; fp32 outputs ||out - ref||_inf / ||ref||_inf <= 1e-5.
+Large workloads are checked on a subset of (batch, head) against the oracle
+(heads are independent) plus size-independent properties on the full
+problem (GQA == repeated KV bit for bit, stride-0 MQA == materialised KV).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention_oracle as orc
+from trinix_amd import triton_attn_func
+from trinix_amd import _native
+from trinix_amd.kernels import TritonAttentionKernel, rope_apply
+from trinix_amd.workloads import WORKLOADS, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def assert_parity(out, ref, dtype, what=""):
+    out = out.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert out.shape == ref.shape, (what, out.shape, ref.shape)
+    nan_o, nan_r = torch.isnan(out), torch.isnan(ref)
+    assert torch.equal(nan_o, nan_r), f"{what}: NaN pattern differs ({int(nan_o.sum())} vs {int(nan_r.sum())})"
+    ok = ~nan_r
+    if not ok.any():
+        return
+    d = (out - ref)[ok].abs()
+    if dtype == torch.float32:
+        rel = (d.max() / ref[ok].abs().max().clamp_min(1e-30)).item()
+        assert rel <= 1e-5, f"{what}: fp32 rel err {rel:.3g} > 1e-5"
+    else:
+        mx, mean = d.max().item(), d.mean().item()
+        assert mx <= 2e-2 and mean <= 2e-3, f"{what}: max abs {mx:.4g} (<=2e-2), mean abs {mean:.4g} (<=2e-3)"
+
+
+def rand(shape, dtype, seed, device=DEV):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype).to(device)
+
+
+def oracle_on(q, k, v, **kw):
+    return orc.functional_attention(q.cpu(), k.cpu(), v.cpu(), **kw)
+
+
+# ---------------------------------------------------------------------------
+# BASELINE workloads
+# ---------------------------------------------------------------------------
+def test_library_loaded_and_device():
+    assert TritonAttentionKernel.is_available()
+    assert _native.library_loaded()
+
+
+def test_c1_fp32_mha():
+    w = WORKLOADS["c1"]
+    inp = make_inputs(w)
+    out = triton_attn_func(inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV))
+    ref = orc.functional_attention(inp.q, inp.k, inp.v)
+    assert out.dtype == torch.float32 and out.shape == inp.q.shape
+    assert_parity(out, ref, torch.float32, "c1")
+
+
+def test_c2_bf16_causal_mha():
+    w = WORKLOADS["c2"]
+    inp = make_inputs(w)
+    out = triton_attn_func(inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV), causal=True)
+    ref = orc.functional_attention(inp.q, inp.k, inp.v, causal=True)
+    assert_parity(out, ref, torch.bfloat16, "c2")
+
+
+def test_c3_gqa_rope_causal_subset():
+    w = WORKLOADS["c3"]
+    inp = make_inputs(w)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    out = triton_attn_func(q, k, v, causal=True, rotary_cos=inp.cos.to(DEV), rotary_sin=inp.sin.to(DEV))
+    assert torch.isfinite(out.float()).all()
+    qr = orc.apply_rope(inp.q, inp.cos, inp.sin)
+    kr = orc.apply_rope(inp.k, inp.cos, inp.sin)
+    heads = [0, 3, 13, 31]
+    ref = orc.functional_attention(qr, kr, inp.v, causal=True, heads=heads)
+    assert_parity(out[:, :, heads], ref, torch.bfloat16, "c3 heads %s" % heads)
+
+
+def test_c4_sliding_window_subset():
+    w = WORKLOADS["c4"]
+    inp = make_inputs(w)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    out = triton_attn_func(q, k, v, causal=True, window_size=w.window, rotary_cos=inp.cos.to(DEV),
+                           rotary_sin=inp.sin.to(DEV))
+    assert torch.isfinite(out.float()).all()
+    qr = orc.apply_rope(inp.q, inp.cos, inp.sin)
+    kr = orc.apply_rope(inp.k, inp.cos, inp.sin)
+    ref = orc.functional_attention(qr, kr, inp.v, causal=True, window_size=w.window, heads=[29], batches=[1])
+    assert_parity(out[1:2, :, [29]], ref, torch.bfloat16, "c4 b1 h29")
+
+
+@pytest.mark.parametrize("name", ["c5a", "c5b"])
+def test_c5_alibi_block_mask_subset(name):
+    w = WORKLOADS[name]
+    inp = make_inputs(w)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    if w.nheads_kv == 1:
+        # MQA as the reference layer feeds it: one KV head expanded (stride 0)
+        k = k.expand(-1, -1, w.nheads, -1)
+        v = v.expand(-1, -1, w.nheads, -1)
+        assert k.stride(2) == 0
+    out = triton_attn_func(q, k, v, attn_mask=inp.mask.to(DEV), alibi_slopes=inp.alibi.to(DEV))
+    heads, batches = [0, 9, 15], [0, 7]
+    ref = orc.functional_attention(inp.q, inp.k, inp.v, attn_mask=inp.mask, alibi_slopes=inp.alibi,
+                                   heads=heads, batches=batches)
+    assert_parity(out[batches][:, :, heads], ref, torch.float16, name)
+
+
+def test_gqa_equals_repeated_kv_bitwise():
+    """C3-sized: GQA kernel on 8 KV heads == kernel on KV repeated to 32 heads."""
+    w = WORKLOADS["c3"]
+    inp = make_inputs(w)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    out_g = triton_attn_func(q, k, v, causal=True)
+    kr = torch.repeat_interleave(k, 4, dim=2)
+    vr = torch.repeat_interleave(v, 4, dim=2)
+    out_r = triton_attn_func(q, kr, vr, causal=True)
+    assert torch.equal(out_g, out_r)
+
+
+def test_mqa_stride0_equals_materialised_bitwise():
+    w = WORKLOADS["c5b"]
+    inp = make_inputs(w)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    m, sl = inp.mask.to(DEV), inp.alibi.to(DEV)
+    a = triton_attn_func(q, k, v, attn_mask=m, alibi_slopes=sl)
+    b = triton_attn_func(q, k.expand(-1, -1, w.nheads, -1), v.expand(-1, -1, w.nheads, -1), attn_mask=m,
+                         alibi_slopes=sl)
+    c = triton_attn_func(q, k.expand(-1, -1, w.nheads, -1).contiguous(), v.expand(-1, -1, w.nheads, -1).contiguous(),
+                         attn_mask=m, alibi_slopes=sl)
+    assert torch.equal(a, b) and torch.equal(a, c)
+
+
+def test_blockmap_is_exact_and_skipping_matches_full_read():
+    w = WORKLOADS["c5a"]
+    inp = make_inputs(w)
+    m4 = TritonAttentionKernel._prepare_mask(inp.mask.to(DEV), w.batch, w.nheads, w.seqlen)
+    bmap, _ = TritonAttentionKernel.mask_blockmap(m4)
+    mc = inp.mask.view(w.seqlen // 32, 32, w.seqlen // 64, 64).permute(0, 2, 1, 3).reshape(w.seqlen // 32, w.seqlen // 64, -1)
+    want = torch.ones(mc.shape[:2], dtype=torch.uint8)
+    want[(mc == 0).all(-1)] = 0
+    want[torch.isneginf(mc).all(-1)] = 2
+    assert torch.equal(bmap.cpu()[0, 0], want)
+    q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
+    a = TritonAttentionKernel.apply(q, k, v, attn_mask=inp.mask.to(DEV), use_blockmap=True)
+    b = TritonAttentionKernel.apply(q, k, v, attn_mask=inp.mask.to(DEV), use_blockmap=False)
+    assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# edge cases against the oracle (small shapes)
+# ---------------------------------------------------------------------------
+CASES = [
+    # (B, Sq, Sk, H, Hkv, D, causal, window)
+    (1, 1, 1, 1, 1, 64, False, None),
+    (2, 100, 100, 3, 3, 64, True, None),
+    (1, 257, 257, 2, 1, 128, True, None),
+    (1, 130, 130, 4, 2, 128, False, (16, 4)),
+    (2, 200, 200, 2, 2, 64, True, (0, 0)),
+    (1, 300, 300, 2, 2, 64, True, (37, 0)),
+    (1, 70, 190, 2, 2, 64, False, None),
+    (1, 190, 70, 2, 2, 128, True, None),
+    (1, 1, 300, 4, 1, 128, False, None),
+    (1, 96, 96, 2, 2, 32, True, None),
+    (1, 96, 96, 2, 2, 80, False, None),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("case", CASES)
+def test_edge_shapes(case, dtype):
+    B, Sq, Sk, H, Hkv, D, causal, window = case
+    q = rand((B, Sq, H, D), dtype, 11)
+    k = rand((B, Sk, Hkv, D), dtype, 12)
+    v = rand((B, Sk, Hkv, D), dtype, 13)
+    out = triton_attn_func(q, k, v, causal=causal, window_size=window)
+    ref = oracle_on(q, k, v, causal=causal, window_size=window)
+    assert_parity(out, ref, dtype, str(case))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("mask_kind", ["2d", "3d", "4d_h1", "4d", "bool2d", "bf16_2d"])
+def test_masks_and_alibi(mask_kind, dtype):
+    B, S, H, D = 2, 160, 4, 64
+    q, k, v = rand((B, S, H, D), dtype, 21), rand((B, S, H, D), dtype, 22), rand((B, S, H, D), dtype, 23)
+    g = torch.Generator().manual_seed(24)
+    if mask_kind == "2d":
+        m = torch.randn((S, S), generator=g)
+        m[torch.rand((S, S), generator=g) < 0.2] = float("-inf")
+    elif mask_kind == "3d":
+        m = torch.randn((B, S, S), generator=g)
+    elif mask_kind == "4d_h1":
+        m = torch.randn((B, 1, S, S), generator=g)
+    elif mask_kind == "4d":
+        m = torch.randn((B, H, S, S), generator=g)
+    elif mask_kind == "bool2d":
+        m = torch.rand((S, S), generator=g) < 0.5
+    else:
+        m = torch.randn((S, S), generator=g).to(torch.bfloat16)
+    slopes = orc.alibi_slopes(H)
+    if m.dtype != torch.bool:
+        m[..., :, 0] = 0  # every row keeps key 0 (allowed under causal)
+    out = triton_attn_func(q, k, v, attn_mask=m.to(DEV), alibi_slopes=slopes.to(DEV), causal=True)
+    mref = m.to(torch.uint8) if m.dtype == torch.bool else m
+    ref = oracle_on(q, k, v, attn_mask=mref.float(), alibi_slopes=slopes, causal=True)
+    assert_parity(out, ref, dtype, mask_kind)
+
+
+def test_leading_tiles_fully_masked_are_exact():
+    """Rows whose first key tiles are all -inf (the reference Triton kernel
+    returns NaN there) match the eager path."""
+    B, S, H, D = 1, 512, 2, 64
+    q, k, v = rand((B, S, H, D), torch.bfloat16, 31), rand((B, S, H, D), torch.bfloat16, 32), rand((B, S, H, D), torch.bfloat16, 33)
+    m = torch.zeros(S, S)
+    m[:, :200] = float("-inf")
+    out = triton_attn_func(q, k, v, attn_mask=m.to(DEV))
+    ref = oracle_on(q, k, v, attn_mask=m)
+    assert_parity(out, ref, torch.bfloat16, "leading masked")
+    out2 = triton_attn_func(q, k, v, causal=True, window_size=(64, 0))
+    ref2 = oracle_on(q, k, v, causal=True, window_size=(64, 0))
+    assert_parity(out2, ref2, torch.bfloat16, "window")
+
+
+def test_fully_masked_rows_give_nan_like_eager():
+    B, S, H, D = 1, 96, 1, 64
+    q, k, v = rand((B, S, H, D), torch.float16, 41), rand((B, S, H, D), torch.float16, 42), rand((B, S, H, D), torch.float16, 43)
+    m = torch.zeros(S, S)
+    m[5] = float("-inf")
+    m[70] = float("-inf")
+    out = triton_attn_func(q, k, v, attn_mask=m.to(DEV))
+    ref = oracle_on(q, k, v, attn_mask=m)
+    assert torch.isnan(ref[0, 5]).all() and torch.isnan(ref[0, 70]).all()
+    assert_parity(out, ref, torch.float16, "nan rows")
+
+
+def test_single_open_column_returns_that_value_row():
+    B, S, H, D = 1, 128, 2, 128
+    q, k, v = rand((B, S, H, D), torch.bfloat16, 51), rand((B, S, H, D), torch.bfloat16, 52), rand((B, S, H, D), torch.bfloat16, 53)
+    m = torch.full((S, S), float("-inf"))
+    m[:, 77] = 0
+    out = triton_attn_func(q, k, v, attn_mask=m.to(DEV))
+    assert torch.equal(out.cpu(), v[:, 77:78].expand(-1, S, -1, -1).cpu())
+
+
+def test_noncontiguous_qkv_from_packed_projection():
+    B, S, H, D = 2, 150, 4, 64
+    qkv = rand((B, S, 3, H, D), torch.bfloat16, 61)
+    q, k, v = qkv.unbind(dim=2)
+    assert not q.is_contiguous()
+    out = triton_attn_func(q, k, v, causal=True)
+    ref = oracle_on(q.contiguous(), k.contiguous(), v.contiguous(), causal=True)
+    assert_parity(out, ref, torch.bfloat16, "packed qkv")
+
+
+def test_lse_output():
+    B, S, H, D = 1, 200, 2, 64
+    q, k, v = rand((B, S, H, D), torch.float32, 71), rand((B, S, H, D), torch.float32, 72), rand((B, S, H, D), torch.float32, 73)
+    out, lse = triton_attn_func(q, k, v, causal=True, return_lse=True)
+    s = torch.einsum("bihd,bjhd->bhij", q.cpu().double(), k.cpu().double()) * D ** -0.5
+    s.masked_fill_(torch.triu(torch.ones(S, S), 1).bool(), float("-inf"))
+    ref = torch.logsumexp(s, dim=-1)
+    assert torch.allclose(lse.cpu().double(), ref, atol=1e-4, rtol=1e-5)
+
+
+def test_runs_on_side_stream():
+    B, S, H, D = 1, 256, 2, 128
+    q, k, v = rand((B, S, H, D), torch.bfloat16, 81), rand((B, S, H, D), torch.bfloat16, 82), rand((B, S, H, D), torch.bfloat16, 83)
+    ref = triton_attn_func(q, k, v, causal=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out = triton_attn_func(q, k, v, causal=True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+# ---------------------------------------------------------------------------
+# RoPE (standalone kernel, bit-exact with the eager rounding sequence)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128, 6])
+def test_rope_bit_exact(dtype, D):
+    B, S, H = 2, 77, 3
+    x = rand((B, S, H, D), dtype, 91)
+    cos, sin = orc.rope_tables(S, D, 10000.0, dtype)
+    out = rope_apply(x, cos.to(DEV), sin.to(DEV))
+    ref = orc.apply_rope(x.cpu(), cos, sin)
+    assert torch.equal(out.cpu(), ref)
+    pos = torch.randint(0, S, (B, S), generator=torch.Generator().manual_seed(92))
+    out2 = rope_apply(x, cos.to(DEV), sin.to(DEV), position_ids=pos.to(DEV))
+    ref2 = orc.apply_rope(x.cpu(), cos, sin, position_ids=pos)
+    assert torch.equal(out2.cpu(), ref2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_fused_rope_matches_prerotated(dtype):
+    B, S, H, Hkv, D = 1, 300, 4, 2, 128
+    q, k, v = rand((B, S, H, D), dtype, 95), rand((B, S, Hkv, D), dtype, 96), rand((B, S, Hkv, D), dtype, 97)
+    cos, sin = orc.rope_tables(S, D, 500000.0, dtype)
+    fused = triton_attn_func(q, k, v, causal=True, rotary_cos=cos.to(DEV), rotary_sin=sin.to(DEV))
+    qr = orc.apply_rope(q.cpu(), cos, sin).to(DEV)
+    kr = orc.apply_rope(k.cpu(), cos, sin).to(DEV)
+    pre = triton_attn_func(qr, kr, v, causal=True)
+    assert torch.equal(fused, pre)
+
+
+# ---------------------------------------------------------------------------
+# dropout: exact against the oracle's Philox stream
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dropout_matches_philox_oracle(dtype):
+    B, S, H, D, p = 1, 128, 2, 64, 0.3
+    q, k, v = rand((B, S, H, D), dtype, 101), rand((B, S, H, D), dtype, 102), rand((B, S, H, D), dtype, 103)
+    torch.manual_seed(1234)
+    out = triton_attn_func(q, k, v, dropout_p=p, causal=True)
+    torch.manual_seed(1234)
+    seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    keep = torch.from_numpy(orc.dropout_keep(B, H, S, S, p, seed)).double()
+    s = torch.einsum("bihd,bjhd->bhij", q.cpu().double(), k.cpu().double()) * D ** -0.5
+    s.masked_fill_(torch.triu(torch.ones(S, S), 1).bool(), float("-inf"))
+    P = torch.softmax(s, dim=-1) * keep / (1 - p)
+    ref = torch.einsum("bhij,bjhd->bihd", P, v.cpu().double())
+    tol = 1e-5 if dtype == torch.float32 else 3e-2
+    assert (out.cpu().double() - ref).abs().max().item() <= tol
+    frac = keep.mean().item()
+    assert abs(frac - (1 - p)) < 0.02

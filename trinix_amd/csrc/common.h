@@ -1,0 +1,85 @@
+// Shared device helpers for the gfx950 attention library: element traits
+// (bf16 / fp16 storage, fp32 math), MFMA wrappers and the workgroup->work
+// mapping across the 8 XCDs of an MI355X.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace trinix {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// 16-bit storage types.  A 32-bit word holds two elements, element 0 in the
+// low half.  pack() rounds to nearest-even (v_cvt_pk_bf16_f32 /
+// v_cvt_pk_f16_f32).  mfma() is D = A*B + C for a 32x32x16 tile: lane l
+// supplies row (l%32) of A and column (l%32) of B, 8 consecutive k each for
+// k-group l/32; D element v of lane l is row (v/4)*8 + (l/32)*4 + v%4,
+// column l%32.
+struct BF16 {
+  __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
+  __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  __device__ static inline uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+  }
+  __device__ static inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  __device__ static inline float lo(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[0]; }
+  __device__ static inline float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
+  __device__ static inline uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+  }
+  __device__ static inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+};
+
+// Round an fp32 value to the storage precision of E and back.
+template <class E>
+__device__ inline float round_to(float x) { return E::lo(E::pack(x, 0.f)); }
+
+// Workgroups are dispatched round-robin over the 8 XCDs (WG x runs on XCD
+// x % 8).  Give each XCD one contiguous range of the work list, so work
+// items that read the same K/V (neighbouring items) share that XCD's L2.
+__device__ inline int xcd_remap(int x, int total) {
+  constexpr int kXcd = 8;
+  const int xcd = x % kXcd, idx = x / kXcd;
+  const int per = total / kXcd, rem = total % kXcd;
+  return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11), the counter-based generator used for dropout.
+struct Philox {
+  __device__ static inline u32x4_t run(u32x4_t c, uint32_t k0, uint32_t k1) {
+    constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+    constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+      const uint32_t hi0 = __umulhi(M0, c[0]), lo0 = M0 * c[0];
+      const uint32_t hi1 = __umulhi(M1, c[2]), lo1 = M1 * c[2];
+      c = (u32x4_t){hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0};
+      k0 += W0;
+      k1 += W1;
+    }
+    return c;
+  }
+};
+
+}  // namespace trinix

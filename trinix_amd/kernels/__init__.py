@@ -1,0 +1,16 @@
+"""HIP kernel wrappers (gfx950); class names kept from the reference registry
+``trinix/kernels/__init__.py:14`` for drop-in use."""
+from .attention_kernel import TritonAttentionKernel, attention_flops, allowed_pairs
+from .rope_kernel import TritonRoPEKernel, rope_apply
+from .utils import calculate_attention_block_sizes, get_cuda_compute_capability, tile_config
+
+__all__ = [
+    "TritonAttentionKernel",
+    "TritonRoPEKernel",
+    "rope_apply",
+    "attention_flops",
+    "allowed_pairs",
+    "calculate_attention_block_sizes",
+    "get_cuda_compute_capability",
+    "tile_config",
+]

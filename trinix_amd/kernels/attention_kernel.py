@@ -1,0 +1,330 @@
+"""Attention forward on MI355X through ``libtrinix_attn.so``.
+
+Host side of the drop-in for ``TritonAttentionKernel``
+(reference ``trinix/kernels/attention_kernel.py:437-664``): same class name,
+same ``is_available()`` / ``apply(...)`` signature, argument meaning and
+output (a new ``(B, Sq, H, D)`` tensor of ``q.dtype``).  Differences, all of
+them inputs the reference rejected or mishandled:
+
+* ``k``/``v`` may carry fewer heads than ``q`` (GQA/MQA, ``H % Hkv == 0``);
+  the kernel maps query head ``h`` to KV head ``h // (H // Hkv)`` without
+  copying (stride-0 ``expand``-ed KV also works without a copy);
+* ``Sq != Sk`` is accepted (causal stays top-left aligned, ``j <= i``, as in
+  the eager path ``trinix/layers/attention/base.py:375-379``);
+* the mask is never materialised to ``(B, H, S, S)``
+  (``attention_kernel.py:479-495``): it is read through broadcast strides and
+  classified once per call into 32x64 blocks;
+* rows whose first key tiles are fully masked are exact (the reference
+  kernel returns NaN there); rows with no allowed key at all give NaN, as
+  the eager softmax does;
+* optional fused RoPE (``rotary_cos`` / ``rotary_sin``) and log-sum-exp
+  output.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from .. import _native as nat
+
+_DTYPE_CODE = {
+    torch.float32: nat.TRINIX_F32,
+    torch.float16: nat.TRINIX_F16,
+    torch.bfloat16: nat.TRINIX_BF16,
+}
+_MASK_DTYPE_CODE = {
+    torch.float32: nat.TRINIX_F32,
+    torch.float16: nat.TRINIX_F16,
+    torch.bfloat16: nat.TRINIX_BF16,
+    torch.uint8: nat.TRINIX_U8,
+}
+KERNEL_HEAD_DIMS = (64, 128)
+
+
+def kernel_head_dim(head_dim: int) -> Optional[int]:
+    """Head dim the kernels run at: inputs are zero-padded up to it."""
+    for d in KERNEL_HEAD_DIMS:
+        if head_dim <= d:
+            return d
+    return None
+
+
+def current_stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _kernel_ready(t: torch.Tensor) -> bool:
+    """True if ``t`` (4-D BSHD) meets the kernel's load constraints as is."""
+    if t.stride(-1) != 1:
+        return False
+    if t.element_size() == 2:
+        if t.data_ptr() % 16:
+            return False
+        return all(s % 8 == 0 for s in t.stride()[:3])
+    return t.data_ptr() % 4 == 0
+
+
+def _prepare_operand(t: torch.Tensor, d_kernel: int) -> torch.Tensor:
+    d = t.shape[-1]
+    if d != d_kernel:
+        t = torch.nn.functional.pad(t, (0, d_kernel - d))
+    if not _kernel_ready(t):
+        t = t.contiguous()
+    return t
+
+
+class TritonAttentionKernel:
+    """MI355X attention forward (name kept from the reference for drop-in use).
+
+    Methods:
+        is_available(): True if the HIP library loads and a gfx950 GPU is
+            visible to torch.
+        apply(q, k, v, attn_mask=None, causal=False, scale=None,
+              dropout_p=0.0, window_size=None, alibi_slopes=None):
+            attention forward; see the module docstring.
+    """
+
+    @staticmethod
+    def is_available() -> bool:
+        try:
+            lib = nat.load_library()
+        except (RuntimeError, OSError):
+            return False
+        if not torch.cuda.is_available():
+            return False
+        return bool(lib.trinix_attn_is_available())
+
+    @staticmethod
+    def _prepare_mask(attn_mask: torch.Tensor, batch_size: int, num_heads: int,
+                      seq_len_q: int, seq_len_k: Optional[int] = None) -> torch.Tensor:
+        """Broadcast view of the mask as (B, H, Sq, Sk), no copy.
+
+        Accepts 2-D (Sq, Sk), 3-D (B, Sq, Sk) and 4-D (B, 1 or H, Sq, Sk)
+        masks like the reference (``attention_kernel.py:479-495``); a size-1
+        batch dimension also broadcasts.
+        """
+        if seq_len_k is None:
+            seq_len_k = seq_len_q
+        if attn_mask.dim() == 2:
+            m = attn_mask[None, None]
+        elif attn_mask.dim() == 3:
+            m = attn_mask[:, None]
+        elif attn_mask.dim() == 4:
+            m = attn_mask
+        else:
+            raise ValueError(f"Unsupported mask shape: {attn_mask.shape}")
+        target = (batch_size, num_heads, seq_len_q, seq_len_k)
+        for have, want in zip(m.shape, target):
+            if have != want and have != 1:
+                raise ValueError(
+                    f"Mask shape {tuple(attn_mask.shape)} doesn't match expected shape {target}"
+                )
+        return m.expand(*target)
+
+    @staticmethod
+    def mask_blockmap(mask4: torch.Tensor, stream: Optional[int] = None) -> Tuple[torch.Tensor, Tuple[int, int]]:
+        """Per-32x64-block classification of a (B, H, Sq, Sk) mask view.
+
+        Returns the uint8 map and its (batch, head) strides; broadcast
+        dimensions of the mask are broadcast in the map too.
+        """
+        B, H, Sq, Sk = mask4.shape
+        mb = B if mask4.stride(0) != 0 else 1
+        mh = H if mask4.stride(1) != 0 else 1
+        rows = -(-Sq // nat.BLOCKMAP_ROWS)
+        cols = -(-Sk // nat.BLOCKMAP_COLS)
+        bmap = torch.empty((mb, mh, rows, cols), dtype=torch.uint8, device=mask4.device)
+        code = _MASK_DTYPE_CODE[mask4.dtype]
+        strides = (ctypes.c_int64 * 4)(*mask4.stride())
+        lib = nat.load_library()
+        if stream is None:
+            stream = current_stream_ptr(mask4.device)
+        rc = lib.trinix_attn_mask_blockmap(mask4.data_ptr(), code, mb, mh, Sq, Sk, strides,
+                                           bmap.data_ptr(), stream)
+        nat.check(rc, "trinix_attn_mask_blockmap")
+        bm_sb = mh * rows * cols if mb > 1 else 0
+        bm_sh = rows * cols if mh > 1 else 0
+        return bmap, (bm_sb, bm_sh)
+
+    @staticmethod
+    def apply(
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        attn_mask: torch.Tensor = None,
+        causal: bool = False,
+        scale: float = None,
+        dropout_p: float = 0.0,
+        window_size: tuple = None,
+        alibi_slopes: torch.Tensor = None,
+        *,
+        rotary_cos: Optional[torch.Tensor] = None,
+        rotary_sin: Optional[torch.Tensor] = None,
+        rotary_k: bool = True,
+        return_lse: bool = False,
+        use_blockmap: bool = True,
+    ):
+        """Attention forward (reference ``attention_kernel.py:497-664``).
+
+        Extensions (keyword-only): ``rotary_cos``/``rotary_sin`` (rows of the
+        reference RoPE tables in ``q.dtype``, indexed by position) apply RoPE
+        to q inside the kernel and to k by a pre-pass (``rotary_k=False``
+        leaves k as given); ``return_lse`` also returns the (B, H, Sq) fp32
+        log-sum-exp.
+        """
+        if not (q.is_cuda and k.is_cuda and v.is_cuda):
+            raise ValueError("TritonAttentionKernel requires GPU tensors")
+        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+            raise ValueError(f"Expected 4D tensors, got q: {q.shape}, k: {k.shape}, v: {v.shape}")
+        if q.dtype not in _DTYPE_CODE:
+            raise ValueError(f"Unsupported dtype {q.dtype}; use float32, float16 or bfloat16")
+        if k.dtype != q.dtype or v.dtype != q.dtype:
+            raise ValueError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
+        B, Sq, H, D = q.shape
+        Bk, Sk, Hkv, Dk = k.shape
+        if Bk != B or Dk != D or tuple(v.shape) != (B, Sk, Hkv, D):
+            raise ValueError(f"k/v shapes {tuple(k.shape)}, {tuple(v.shape)} don't match q {tuple(q.shape)}")
+        if Hkv <= 0 or H % Hkv != 0:
+            raise ValueError(f"num_heads ({H}) must be a multiple of the KV heads ({Hkv})")
+        d_kernel = kernel_head_dim(D)
+        if d_kernel is None:
+            raise ValueError(f"head_dim {D} > {KERNEL_HEAD_DIMS[-1]} is not supported")
+        if not (0.0 <= dropout_p < 1.0):
+            raise ValueError(f"dropout_p must be in [0, 1), got {dropout_p}")
+        if scale is None:
+            scale = D ** -0.5
+        device = q.device
+        stream = current_stream_ptr(device)
+        lib = nat.load_library()
+
+        if rotary_cos is not None or rotary_sin is not None:
+            if rotary_cos is None or rotary_sin is None:
+                raise ValueError("rotary_cos and rotary_sin must be given together")
+            if D % 2:
+                raise ValueError("RoPE needs an even head_dim")
+            if rotary_cos.shape[0] < max(Sq, Sk) or rotary_cos.shape[-1] < D // 2:
+                raise ValueError("rotary tables are smaller than (seq_len, head_dim/2)")
+            if rotary_k:
+                from .rope_kernel import rope_apply
+                k = rope_apply(k, rotary_cos, rotary_sin)
+            if d_kernel != D:
+                # RoPE pairs (d, d + D/2) of the unpadded head dim: rotate q
+                # here, then pad, rather than fusing at the padded width.
+                from .rope_kernel import rope_apply
+                q = rope_apply(q, rotary_cos, rotary_sin)
+                rotary_cos = rotary_sin = None
+
+        qk = _prepare_operand(q, d_kernel)
+        kk = _prepare_operand(k, d_kernel)
+        vk = _prepare_operand(v, d_kernel)
+        out = torch.empty((B, Sq, H, d_kernel), dtype=q.dtype, device=device)
+
+        args = nat.AttnFwdArgs()
+        args.q, args.k, args.v, args.out = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
+        lse = None
+        if return_lse:
+            lse = torch.empty((B, H, Sq), dtype=torch.float32, device=device)
+            args.lse = lse.data_ptr()
+        args.q_stride = nat.int64x4(qk.stride())
+        args.k_stride = nat.int64x4(kk.stride())
+        args.v_stride = nat.int64x4(vk.stride())
+        args.out_stride = nat.int64x4(out.stride())
+        args.batch, args.seqlen_q, args.seqlen_k = B, Sq, Sk
+        args.nheads_q, args.nheads_kv, args.head_dim = H, Hkv, d_kernel
+        args.dtype = _DTYPE_CODE[q.dtype]
+        args.softmax_scale = float(scale)
+        args.causal = 1 if causal else 0
+        if window_size is not None:
+            wl, wr = window_size
+            args.has_window = 1
+            args.window_left, args.window_right = int(wl), int(wr)
+
+        keep = [qk, kk, vk]  # hold references until the launch returns
+        if alibi_slopes is not None:
+            sl = alibi_slopes
+            if sl.dim() == 1:
+                sl = sl.unsqueeze(0)
+            if sl.dim() != 2 or sl.shape[-1] != H or sl.shape[0] not in (1, B):
+                raise ValueError(f"alibi_slopes shape {tuple(alibi_slopes.shape)} must be (H,), (1, H) or (B, H)")
+            sl = sl.to(device=device, dtype=torch.float32).contiguous()
+            keep.append(sl)
+            args.alibi_slopes = sl.data_ptr()
+            args.alibi_stride = nat.int64x2((H if sl.shape[0] > 1 else 0, 1))
+
+        if attn_mask is not None:
+            m = attn_mask
+            if m.device != device:
+                m = m.to(device)
+            if m.dtype == torch.bool:
+                m = m.view(torch.uint8)
+            elif m.dtype not in _MASK_DTYPE_CODE:
+                m = m.to(torch.float32)
+            m4 = TritonAttentionKernel._prepare_mask(m, B, H, Sq, Sk)
+            keep.append(m4)
+            args.mask = m4.data_ptr()
+            args.mask_dtype = _MASK_DTYPE_CODE[m4.dtype]
+            args.mask_stride = nat.int64x4(m4.stride())
+            if use_blockmap:
+                bmap, bst = TritonAttentionKernel.mask_blockmap(m4, stream)
+                keep.append(bmap)
+                args.mask_blockmap = bmap.data_ptr()
+                args.blockmap_stride = nat.int64x2(bst)
+
+        if dropout_p > 0.0:
+            # Seed from torch's CPU generator: no device->host sync.
+            args.dropout_p = float(dropout_p)
+            args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+            args.dropout_offset = 0
+
+        if rotary_cos is not None:
+            cos = rotary_cos.to(device=device, dtype=q.dtype)
+            sin = rotary_sin.to(device=device, dtype=q.dtype)
+            if cos.stride(-1) != 1 or cos.stride(0) % 8 or cos.data_ptr() % 16:
+                cos = cos.contiguous()
+            if sin.stride(-1) != 1 or sin.stride(0) != cos.stride(0) or sin.data_ptr() % 16:
+                sin = sin.contiguous()
+                if sin.stride(0) != cos.stride(0):
+                    cos = cos.contiguous()
+            keep += [cos, sin]
+            args.rope_cos, args.rope_sin, args.rope_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+
+        rc = lib.trinix_attn_fwd(ctypes.byref(args), stream)
+        nat.check(rc, "trinix_attn_fwd")
+        if d_kernel != D:
+            out = out[..., :D].contiguous()
+        if return_lse:
+            return out, lse
+        return out
+
+
+def attention_flops(batch: int, nheads: int, seqlen_q: int, seqlen_k: int, head_dim: int,
+                    causal: bool = False, window_size: Optional[Tuple[int, int]] = None) -> int:
+    """Algorithmic FLOP = 4 * D * (allowed (i, j) pairs), summed over (b, h).
+
+    Masked-out pairs are not counted.  Pairs follow the kernel's predicate:
+    j < Sk, j <= i if causal, -wl <= j - i <= wr with a window.
+    """
+    return 4 * head_dim * batch * nheads * allowed_pairs(seqlen_q, seqlen_k, causal, window_size)
+
+
+def allowed_pairs(seqlen_q: int, seqlen_k: int, causal: bool = False,
+                  window_size: Optional[Tuple[int, int]] = None) -> int:
+    """Number of (i, j) with 0 <= i < Sq, 0 <= j < Sk allowed by causal/window."""
+    lo_off = -math.inf
+    hi_off = math.inf
+    if window_size is not None:
+        lo_off, hi_off = -window_size[0], window_size[1]
+    if causal:
+        hi_off = min(hi_off, 0)
+    if lo_off == -math.inf and hi_off == math.inf:
+        return seqlen_q * seqlen_k
+    # per row i: j in [max(0, i + lo_off), min(Sk - 1, i + hi_off)]
+    import numpy as np
+
+    i = np.arange(seqlen_q, dtype=np.int64)
+    lo = np.zeros_like(i) if lo_off == -math.inf else np.maximum(0, i + int(lo_off))
+    hi = np.full_like(i, seqlen_k - 1) if hi_off == math.inf else np.minimum(seqlen_k - 1, i + int(hi_off))
+    return int(np.clip(hi - lo + 1, 0, None).sum())
