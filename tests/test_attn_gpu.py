@@ -43,6 +43,24 @@ def assert_parity(out, ref, dtype, what=""):
         assert mx <= 2e-2 and mean <= 2e-3, f"{what}: max abs {mx:.4g} (<=2e-2), mean abs {mean:.4g} (<=2e-3)"
 
 
+def assert_parity_or_more_accurate(out, ref, x64, dtype, what=""):
+    """Parity with the eager oracle.  Where the oracle's own rounding of the
+    biased scores to the input dtype (reference base.py:392 adds the fp32
+    mask/ALiBi bias in place into bf16/fp16 scores) already costs more than
+    half of the max-abs budget against the fp64 closed form, the kernel, which
+    adds biases in fp32, must instead meet the budget against the fp64 closed
+    form and be at least as accurate as the oracle."""
+    x64 = torch.as_tensor(x64).float()
+    ok = ~torch.isnan(x64)
+    o_err = (ref.float().cpu() - x64)[ok].abs().max().item()
+    if dtype != torch.float32 and o_err > 1e-2:
+        assert_parity(out, x64, dtype, what + " (vs fp64)")
+        k_err = (out.float().cpu() - x64)[ok].abs().max().item()
+        assert k_err <= o_err, f"{what}: kernel err {k_err:.4g} > oracle err {o_err:.4g} vs fp64"
+    else:
+        assert_parity(out, ref, dtype, what)
+
+
 def rand(shape, dtype, seed, device=DEV):
     g = torch.Generator().manual_seed(seed)
     return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype).to(device)
@@ -189,7 +207,8 @@ def test_edge_shapes(case, dtype):
     v = rand((B, Sk, Hkv, D), dtype, 13)
     out = triton_attn_func(q, k, v, causal=causal, window_size=window)
     ref = oracle_on(q, k, v, causal=causal, window_size=window)
-    assert_parity(out, ref, dtype, str(case))
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), causal=causal, window_size=window)
+    assert_parity_or_more_accurate(out, ref, x64, dtype, str(case))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
@@ -217,7 +236,8 @@ def test_masks_and_alibi(mask_kind, dtype):
     out = triton_attn_func(q, k, v, attn_mask=m.to(DEV), alibi_slopes=slopes.to(DEV), causal=True)
     mref = m.to(torch.uint8) if m.dtype == torch.bool else m
     ref = oracle_on(q, k, v, attn_mask=mref.float(), alibi_slopes=slopes, causal=True)
-    assert_parity(out, ref, dtype, mask_kind)
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), attn_mask=mref.float(), alibi_slopes=slopes, causal=True)
+    assert_parity_or_more_accurate(out, ref, x64, dtype, mask_kind)
 
 
 def test_leading_tiles_fully_masked_are_exact():
@@ -229,10 +249,12 @@ def test_leading_tiles_fully_masked_are_exact():
     m[:, :200] = float("-inf")
     out = triton_attn_func(q, k, v, attn_mask=m.to(DEV))
     ref = oracle_on(q, k, v, attn_mask=m)
-    assert_parity(out, ref, torch.bfloat16, "leading masked")
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), attn_mask=m)
+    assert_parity_or_more_accurate(out, ref, x64, torch.bfloat16, "leading masked")
     out2 = triton_attn_func(q, k, v, causal=True, window_size=(64, 0))
     ref2 = oracle_on(q, k, v, causal=True, window_size=(64, 0))
-    assert_parity(out2, ref2, torch.bfloat16, "window")
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), causal=True, window_size=(64, 0))
+    assert_parity_or_more_accurate(out2, ref2, x64, torch.bfloat16, "window")
 
 
 def test_fully_masked_rows_give_nan_like_eager():

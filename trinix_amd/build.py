@@ -51,24 +51,50 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the HIP library; returns the path of the built ``.so``."""
+def _compile_flags() -> list[str]:
+    return [*HIPCC_FLAGS, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}"]
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> Path:
+    """Compile every csrc/*.hip to an object (in parallel), then link the
+    shared library; returns the path of the built ``.so``."""
     LIB_DIR.mkdir(parents=True, exist_ok=True)
+    obj_dir = LIB_DIR / "_obj"
+    obj_dir.mkdir(exist_ok=True)
+    hipcc = hipcc_path()
+    cflags = [f for f in _compile_flags() if f != "-shared"]
+    srcs = sources()
+    objs = [obj_dir / (s.stem + ".o") for s in srcs]
+    jobs = jobs or max(1, min(len(srcs), os.cpu_count() or 1, 8))
+    pending = list(zip(srcs, objs))
+    running = []
+    errors = []
+    while pending or running:
+        while pending and len(running) < jobs:
+            src, obj = pending.pop(0)
+            cmd = [hipcc, *cflags, "-c", str(src), "-o", str(obj)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            running.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+        src, proc = running.pop(0)
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            errors.append(f"{src.name}:\n{err[-6000:]}")
+        elif verbose:
+            lines = [l for l in err.splitlines() if "packed-fp32-ops" not in l]
+            if lines:
+                print("\n".join(lines[-40:]), file=sys.stderr)
+    if errors:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(errors))
     tmp = LIB_DIR / (LIB_NAME + f".tmp{os.getpid()}")
-    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}",
-           *map(str, sources()), "-o", str(tmp)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         if tmp.exists():
             tmp.unlink()
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-8000:]}")
-    if verbose and res.stderr.strip():
-        # hipcc's host pass warns about the device-only target feature
-        lines = [l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l]
-        if lines:
-            print("\n".join(lines[-40:]), file=sys.stderr)
+        raise RuntimeError(f"link failed ({res.returncode}):\n{res.stderr[-8000:]}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -1,71 +1,22 @@
-// Attention forward for MI355X (gfx950): online-softmax attention with
-// MFMA QK^T / PV, LDS-staged double-buffered K/V tiles, in-kernel causal /
-// sliding-window / ALiBi / additive-mask handling with masked-tile skipping,
-// GQA/MQA head mapping through strides, fused RoPE on q and optional dropout.
+// Host entry points of the attention library (C ABI) and the fp32 kernel.
 //
-// Semantics follow the reference Triton kernels
-//   trinix/kernels/attention_kernel.py:123-216 (_fwd_kernel_with_mask) and
-//   :341-416 (_fwd_kernel):
-//     s = q.k * scale; s += -slope*|i-j|; s += mask; s = -inf where
-//     disallowed (causal j<=i, window -wl<=j-i<=wr, j<Sk); online softmax;
-//     p rounded to the input dtype before the PV product; out = acc / l.
-// with the eager path's normalisation for dropout
-// (trinix/layers/attention/base.py:394-397: softmax, then dropout, then PV),
-// and a guard for rows whose leading tiles are fully masked.
+// trinix_attn_fwd validates the arguments, picks a tile configuration for
+// (dtype, head_dim, problem size), the feature flags (ALiBi, mask, dropout)
+// and launches the bf16/fp16 MFMA kernel (attn_kernel16.h, instantiated per
+// (dtype, head_dim) in attn16_*.hip) or the fp32 kernel below.
 //
-// Work decomposition (16-bit inputs): one workgroup = NW wavefronts, one
-// (batch, q-head, block of 32*NW query rows).  Each wavefront owns 32 query
-// rows and computes S^T = K Q^T (keys on MFMA rows, queries on columns) so a
-// lane holds one query row; the row max / sum need one cross-lane exchange
-// (lane ^ 32).  O^T = V^T P^T reuses the S^T register layout as the B operand
-// directly; V is stored transposed in LDS for the A operand.
+// The fp32 kernel uses v_mfma_f32_32x32x2f32 (exact fp32 products, fp32
+// sums) with one 32-key tile at a time and K/V row-major in LDS; it follows
+// the same semantics and work decomposition as the 16-bit kernel
+// (reference trinix/kernels/attention_kernel.py:123-216, :341-416).
 #include <cstring>
 
-#include "common.h"
-#include "trinix_attn.h"
+#include <cstdio>
+#include <cstdlib>
+
+#include "attn_params.h"
 
 namespace trinix {
-
-struct FwdParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  uint16_t* o;
-  float* lse;
-  int64_t q_sb, q_ss, q_sh;
-  int64_t k_sb, k_ss, k_sh;
-  int64_t v_sb, v_ss, v_sh;
-  int64_t o_sb, o_ss, o_sh;
-  int B, Sq, Sk, Hq, Hkv, G;
-  int num_mblk, total_work;
-  float scale_log2;  // softmax_scale * log2(e)
-  int causal, has_window;
-  int64_t wl, wr;
-  const float* alibi;
-  int64_t al_sb, al_sh;
-  const void* mask;
-  int mask_dtype;
-  int64_t mk_sb, mk_sh, mk_si, mk_sj;
-  const uint8_t* bmap;
-  int64_t bm_sb, bm_sh;
-  int bm_cols;
-  int use_dropout;
-  uint32_t drop_thresh;  // drop when philox word < drop_thresh
-  float drop_scale;      // 1 / (1 - p)
-  uint32_t seed_lo, seed_hi, off_lo, off_hi;
-  const uint16_t* rope_cos;
-  const uint16_t* rope_sin;
-  int64_t rope_stride;
-};
-
-__device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx) {
-  switch (dtype) {
-    case TRINIX_F32: return ((const float*)base)[idx];
-    case TRINIX_F16: return (float)((const _Float16*)base)[idx];
-    case TRINIX_BF16: return __uint_as_float(((uint32_t)((const uint16_t*)base)[idx]) << 16);
-    default: return (float)((const uint8_t*)base)[idx];
-  }
-}
 
 // Applies scale, ALiBi, the additive mask and the allowed-pair predicate to a
 // group of 4 consecutive keys j0..j0+3 of query row i, in the log2 domain.
@@ -90,14 +41,6 @@ __device__ inline void score_group(float* x, const FwdParams& p, int i, int ic, 
     x[e] = y;
   }
   (void)ic;
-}
-
-// Dropout on 4 consecutive keys j0..j0+3 of row i: p <- keep ? p/(1-p) : 0.
-__device__ inline void dropout_group(float* x, const FwdParams& p, int bh, int i, int j0) {
-  const u32x4_t c = {(uint32_t)(j0 >> 2), (uint32_t)i, (uint32_t)bh, p.off_lo};
-  const u32x4_t r = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) x[e] = (r[e] < p.drop_thresh) ? 0.f : x[e] * p.drop_scale;
 }
 
 // Per-wavefront decision for one K/V tile [n0, n0+BN) against rows
@@ -138,280 +81,6 @@ __device__ inline int classify_tile(const FwdParams& p, int b, int hq, int iw0, 
   }
   return flags;
 }
-
-template <class E, int D, int BN, int NW>
-__global__ __launch_bounds__(NW * 64, 2) void attn_fwd_mfma16(const FwdParams p) {
-  constexpr int NT = NW * 64;
-  constexpr int BM = NW * 32;
-  constexpr int DS = D / 16;  // MFMA k-steps over head_dim for QK^T
-  constexpr int NB = BN / 32; // 32-key blocks per tile
-  constexpr int DB = D / 32;  // 32-wide head_dim blocks of O^T
-  constexpr int KCH = BN * D / 8;
-  constexpr int KPT = (KCH + NT - 1) / NT;
-  constexpr int VBLK = BN * D / 32;
-  constexpr int VPT = (VBLK + NT - 1) / NT;
-  static_assert(D % 64 == 0 && BN % 64 == 0, "tile shape");
-
-  // K tile: row-major [key][D], 16-byte units XOR-swizzled by (key & 7).
-  // V tile: transposed [d][BN]; within each 16-key chunk, key 8a+4g+e sits at
-  // position 8g+4a+e so that one 16-byte read returns exactly the 8 keys a
-  // lane of k-group g feeds to the PV MFMA; units XOR-swizzled by (d & 7).
-  __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][D * BN];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int r = lane & 31, g = lane >> 5;
-
-  int w = xcd_remap(blockIdx.x, p.total_work);
-  const int gq = w % p.G;
-  w /= p.G;
-  const int mi = w % p.num_mblk;
-  w /= p.num_mblk;
-  const int hkv = w % p.Hkv;
-  const int b = w / p.Hkv;
-  const int hq = hkv * p.G + gq;
-  const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
-  const int m0 = mblk * BM;
-  const int iw0 = m0 + wave * 32;
-  const int iwl = min(iw0 + 31, p.Sq - 1);
-  const int i = iw0 + r;
-  const int ic = min(i, p.Sq - 1);
-
-  // Key range of the workgroup.
-  const int mlast = min(m0 + BM, p.Sq) - 1;
-  int64_t lo = 0, hi = p.Sk;
-  if (p.causal) hi = min(hi, (int64_t)mlast + 1);
-  if (p.has_window) {
-    lo = max(lo, (int64_t)m0 - p.wl);
-    hi = min(hi, (int64_t)mlast + p.wr + 1);
-  }
-  const int t_lo = (int)(lo / BN);
-  const int t_hi = hi > lo ? (int)((hi + BN - 1) / BN) : t_lo;
-
-  // Q rows in registers: qr[ds] = q[i][ds*16 + g*8 .. +8].
-  u32x4_t qr[DS];
-  {
-    const uint16_t* qrow = p.q + b * p.q_sb + hq * p.q_sh + (int64_t)ic * p.q_ss;
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qr[ds] = *(const u32x4_t*)(qrow + ds * 16 + g * 8);
-    if (p.rope_cos) {
-      // Fused RoPE (reference trinix/layers/embeddings/rope.py:111-118):
-      // x*cos + rotate_half(x)*sin with each product and the sum rounded to
-      // the input dtype, as eager PyTorch evaluates it.  d and d + D/2 share
-      // cos/sin and sit in the same lane (chunks ds and ds + DS/2).
-      const uint16_t* crow = p.rope_cos + (int64_t)ic * p.rope_stride;
-      const uint16_t* srow = p.rope_sin + (int64_t)ic * p.rope_stride;
-#pragma unroll
-      for (int ds = 0; ds < DS / 2; ++ds) {
-        const u32x4_t cw = *(const u32x4_t*)(crow + ds * 16 + g * 8);
-        const u32x4_t sw = *(const u32x4_t*)(srow + ds * 16 + g * 8);
-        u32x4_t x1 = qr[ds], x2 = qr[ds + DS / 2];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float c0 = E::lo(cw[e]), c1 = E::hi(cw[e]);
-          const float s0 = E::lo(sw[e]), s1 = E::hi(sw[e]);
-          const float a0 = E::lo(x1[e]), a1 = E::hi(x1[e]);
-          const float b0 = E::lo(x2[e]), b1 = E::hi(x2[e]);
-          const float n0 = round_to<E>(round_to<E>(a0 * c0) - round_to<E>(b0 * s0));
-          const float n1 = round_to<E>(round_to<E>(a1 * c1) - round_to<E>(b1 * s1));
-          const float m0_ = round_to<E>(round_to<E>(b0 * c0) + round_to<E>(a0 * s0));
-          const float m1_ = round_to<E>(round_to<E>(b1 * c1) + round_to<E>(a1 * s1));
-          x1[e] = E::pack(n0, n1);
-          x2[e] = E::pack(m0_, m1_);
-        }
-        qr[ds] = x1;
-        qr[ds + DS / 2] = x2;
-      }
-    }
-  }
-
-  f32x16_t acc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) acc[db] = (f32x16_t){};
-  float m_run = -INFINITY, l_run = 0.f;
-  const float slope_l2 = p.alibi ? -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e : 0.f;
-  const char* mrow = nullptr;
-  if (p.mask) {
-    const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
-    mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)ic * p.mk_si) * esz;
-  }
-
-  const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
-  const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  u32x4_t kst[KPT];
-  u32x4_t vst[VPT][4];
-
-  auto gload = [&](int tile) {
-    const int n0 = tile * BN;
-#pragma unroll
-    for (int t = 0; t < KPT; ++t) {
-      const int c = tid + t * NT;
-      if (c < KCH) {
-        const int key = c / (D / 8), unit = c % (D / 8);
-        const int j = n0 + key;
-        kst[t] = j < p.Sk ? *(const u32x4_t*)(kbase + (int64_t)j * p.k_ss + unit * 8) : (u32x4_t){};
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < VPT; ++t) {
-      const int blk = tid + t * NT;
-      if (blk < VBLK) {
-        const int kg = blk % (BN / 4), dch = blk / (BN / 4);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int j = n0 + kg * 4 + rr;
-          vst[t][rr] = j < p.Sk ? *(const u32x4_t*)(vbase + (int64_t)j * p.v_ss + dch * 8) : (u32x4_t){};
-        }
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int t = 0; t < KPT; ++t) {
-      const int c = tid + t * NT;
-      if (c < KCH) {
-        const int key = c / (D / 8), unit = c % (D / 8);
-        *(u32x4_t*)(&lds_k[buf][key * D + ((unit ^ (key & 7)) * 8)]) = kst[t];
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < VPT; ++t) {
-      const int blk = tid + t * NT;
-      if (blk < VBLK) {
-        const int kg = blk % (BN / 4), dch = blk / (BN / 4);
-        const int c16 = kg >> 2, a = (kg >> 1) & 1, gg = kg & 1;
-#pragma unroll
-        for (int dd = 0; dd < 8; ++dd) {
-          const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t w0 = __builtin_amdgcn_perm(vst[t][1][dd >> 1], vst[t][0][dd >> 1], sel);
-          const uint32_t w1 = __builtin_amdgcn_perm(vst[t][3][dd >> 1], vst[t][2][dd >> 1], sel);
-          const int d = dch * 8 + dd;
-          const int unit = (2 * c16 + gg) ^ (d & 7);
-          *(u32x2_t*)(&lds_v[buf][d * BN + unit * 8 + a * 4]) = (u32x2_t){w0, w1};
-        }
-      }
-    }
-  };
-
-  if (t_lo < t_hi) gload(t_lo);
-  int buf = 0;
-  for (int t = t_lo; t < t_hi; ++t) {
-    lstore(buf);
-    __syncthreads();
-    if (t + 1 < t_hi) gload(t + 1);
-    const int n0 = t * BN;
-    const int cls = iw0 < p.Sq ? classify_tile<BN>(p, b, hq, iw0, iwl, n0) : 0;
-    if (cls) {
-      f32x16_t s[NB];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        s[nb] = (f32x16_t){};
-        const int row = nb * 32 + r;
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-          const int unit = (ds * 2 + g) ^ (row & 7);
-          const u32x4_t a = *(const u32x4_t*)(&lds_k[buf][row * D + unit * 8]);
-          s[nb] = E::mfma(a, qr[ds], s[nb]);
-        }
-      }
-      const bool pred = cls & 2, use_mask = cls & 4;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-          float x[4] = {s[nb][vq * 4 + 0], s[nb][vq * 4 + 1], s[nb][vq * 4 + 2], s[nb][vq * 4 + 3]};
-          const int j0 = n0 + nb * 32 + vq * 8 + g * 4;
-          if (pred) score_group<true>(x, p, i, ic, j0, slope_l2, mrow, use_mask);
-          else score_group<false>(x, p, i, ic, j0, slope_l2, mrow, use_mask);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            s[nb][vq * 4 + e] = x[e];
-            mx = fmaxf(mx, x[e]);
-          }
-        }
-      }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-      float rs = 0.f;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float e = __builtin_amdgcn_exp2f(s[nb][v] - m_use);
-          s[nb][v] = e;
-          rs += e;
-        }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-      if (p.use_dropout) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int vq = 0; vq < 4; ++vq) {
-            float x[4] = {s[nb][vq * 4 + 0], s[nb][vq * 4 + 1], s[nb][vq * 4 + 2], s[nb][vq * 4 + 3]};
-            dropout_group(x, p, b * p.Hq + hq, i, n0 + nb * 32 + vq * 8 + g * 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = x[e];
-          }
-      }
-#pragma unroll
-      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
-      u32x4_t pb[NB][2];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          pb[nb][kk] = (u32x4_t){E::pack(s[nb][kk * 8 + 0], s[nb][kk * 8 + 1]),
-                                 E::pack(s[nb][kk * 8 + 2], s[nb][kk * 8 + 3]),
-                                 E::pack(s[nb][kk * 8 + 4], s[nb][kk * 8 + 5]),
-                                 E::pack(s[nb][kk * 8 + 6], s[nb][kk * 8 + 7])};
-#pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int d = db * 32 + r;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            const int unit = (2 * (2 * nb + kk) + g) ^ (d & 7);
-            const u32x4_t a = *(const u32x4_t*)(&lds_v[buf][d * BN + unit * 8]);
-            acc[db] = E::mfma(a, pb[nb][kk], acc[db]);
-          }
-      }
-    }
-    buf ^= 1;
-  }
-
-  // Epilogue: O = acc / l (NaN for rows with no allowed key, as the eager
-  // softmax over an all -inf row gives), optional log-sum-exp.
-  const float l = l_run + __shfl_xor(l_run, 32);
-  if (i < p.Sq) {
-    const float inv = 1.f / l;
-    uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)i * p.o_ss;
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int vq = 0; vq < 4; ++vq) {
-        const int d0 = db * 32 + vq * 8 + g * 4;
-        const u32x2_t w2 = {E::pack(acc[db][vq * 4 + 0] * inv, acc[db][vq * 4 + 1] * inv),
-                            E::pack(acc[db][vq * 4 + 2] * inv, acc[db][vq * 4 + 3] * inv)};
-        *(u32x2_t*)(orow + d0) = w2;
-      }
-    if (p.lse && g == 0) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = (m_run + __log2f(l)) * kLn2;
-  }
-}
-
-// fp32 inputs: v_mfma_f32_32x32x2f32 (exact fp32 products, fp32 sums), one
-// 32-key tile at a time, K and V row-major in LDS.  Same decomposition and
-// semantics as the 16-bit kernel.
-struct FwdParamsF32Ptrs {
-  const float* q;
-  const float* k;
-  const float* v;
-  float* o;
-};
 
 template <int D, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
@@ -461,6 +130,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
 #pragma unroll
     for (int ds = 0; ds < D / 2; ++ds) qf[ds] = qrow[2 * ds + g];
     if (p.rope_cos) {
+#pragma clang fp contract(off)
       const float* crow = (const float*)p.rope_cos + (int64_t)ic * p.rope_stride;
       const float* srow = (const float*)p.rope_sin + (int64_t)ic * p.rope_stride;
 #pragma unroll
@@ -469,8 +139,8 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
         const float c = crow[d], s = srow[d];
         const float x1 = qf[ds], x2 = qf[ds + D / 4];
         // separate roundings, as eager PyTorch's mul / add kernels
-        qf[ds] = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-        qf[ds + D / 4] = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+        qf[ds] = x1 * c - x2 * s;
+        qf[ds + D / 4] = x2 * c + x1 * s;
       }
     }
   }
@@ -584,8 +254,6 @@ using namespace trinix;
 
 namespace {
 
-constexpr int kBlockN = 64;
-constexpr int kWaves16 = 4;
 constexpr int kWavesF32 = 4;
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -604,14 +272,20 @@ int check_tensor(const void* ptr, const int64_t st[4], int esize) {
   return TRINIX_OK;
 }
 
-template <class E, int D>
-void launch16(const FwdParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_mfma16<E, D, kBlockN, kWaves16>), grid, dim3(kWaves16 * 64), 0, st, p);
-}
-
-template <int D>
-void launchf32(const FwdParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_f32<D, kWavesF32>), grid, dim3(kWavesF32 * 64), 0, st, p);
+// Tile configuration of the 16-bit kernel: 4 wavefronts x 32 query rows,
+// 64-key tiles.  TRINIX_ATTN_CFG="nw,qb,bn" overrides the choice (tuning
+// only; a configuration that is not built is rejected with
+// TRINIX_ERR_BAD_ARGUMENT).
+Cfg16 pick_cfg16(int64_t batch, int64_t hq, int64_t sq) {
+  Cfg16 c{4, 1, 64};
+  (void)batch;
+  (void)hq;
+  (void)sq;
+  if (const char* env = getenv("TRINIX_ATTN_CFG")) {
+    int nw = 0, qb = 0, bn = 0;
+    if (sscanf(env, "%d,%d,%d", &nw, &qb, &bn) == 3) c = Cfg16{nw, qb, bn};
+  }
+  return c;
 }
 
 }  // namespace
@@ -649,11 +323,12 @@ int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* ou
   if (!out) return TRINIX_ERR_NULL_POINTER;
   if (head_dim != 64 && head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
   if (dtype == TRINIX_BF16 || dtype == TRINIX_F16) {
-    out->block_m = 32 * kWaves16;
-    out->block_n = kBlockN;
+    const Cfg16 c = pick_cfg16(1 << 20, 1, 1 << 20);  // large-problem choice
+    out->block_m = 32 * c.nw * c.qb;
+    out->block_n = c.bn;
     out->block_d = (int32_t)head_dim;
-    out->waves = kWaves16;
-    out->lds_bytes = (int32_t)(2 * 2 * kBlockN * head_dim * 2);
+    out->waves = c.nw;
+    out->lds_bytes = (int32_t)(2 * 2 * c.bn * head_dim * 2);
   } else if (dtype == TRINIX_F32) {
     out->block_m = 32 * kWavesF32;
     out->block_n = 32;
@@ -707,7 +382,9 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.Hq = (int)a->nheads_q;
   p.Hkv = (int)a->nheads_kv;
   p.G = p.Hq / p.Hkv;
-  const int bm = 32 * (a->dtype == TRINIX_F32 ? kWavesF32 : kWaves16);
+  const bool f32 = a->dtype == TRINIX_F32;
+  const Cfg16 cfg = pick_cfg16(a->batch, a->nheads_q, a->seqlen_q);
+  const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw * cfg.qb;
   p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
   const int64_t total = (int64_t)p.B * p.Hq * p.num_mblk;
   if (total >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
@@ -742,19 +419,22 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.rope_stride = a->rope_stride;
 
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid((unsigned)p.total_work);
   (void)hipGetLastError();
-  if (a->dtype == TRINIX_BF16) {
-    if (a->head_dim == 64) launch16<BF16, 64>(p, grid, st);
-    else launch16<BF16, 128>(p, grid, st);
-  } else if (a->dtype == TRINIX_F16) {
-    if (a->head_dim == 64) launch16<F16, 64>(p, grid, st);
-    else launch16<F16, 128>(p, grid, st);
+  hipError_t err;
+  if (f32) {
+    const dim3 grid((unsigned)p.total_work), block(kWavesF32 * 64);
+    if (a->head_dim == 64) hipLaunchKernelGGL((attn_fwd_f32<64, kWavesF32>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((attn_fwd_f32<128, kWavesF32>), grid, block, 0, st, p);
+    err = hipGetLastError();
   } else {
-    if (a->head_dim == 64) launchf32<64>(p, grid, st);
-    else launchf32<128>(p, grid, st);
+    const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0);
+    if (a->dtype == TRINIX_BF16)
+      err = a->head_dim == 64 ? launch_attn16_bf16_d64(p, cfg, feat, st) : launch_attn16_bf16_d128(p, cfg, feat, st);
+    else
+      err = a->head_dim == 64 ? launch_attn16_f16_d64(p, cfg, feat, st) : launch_attn16_f16_d128(p, cfg, feat, st);
+    if (err == hipErrorInvalidValue) return TRINIX_ERR_BAD_ARGUMENT;  // tile config not built
   }
-  return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+  return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }
 
 }  // extern "C"

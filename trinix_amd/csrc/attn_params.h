@@ -1,0 +1,90 @@
+// Launch parameters of the attention kernels and the small device helpers
+// they share (mask element loads, dropout, cross-lane reductions).
+#pragma once
+#include "common.h"
+#include "trinix_attn.h"
+
+namespace trinix {
+
+struct FwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  float* lse;
+  int64_t q_sb, q_ss, q_sh;
+  int64_t k_sb, k_ss, k_sh;
+  int64_t v_sb, v_ss, v_sh;
+  int64_t o_sb, o_ss, o_sh;
+  int B, Sq, Sk, Hq, Hkv, G;
+  int num_mblk, total_work;
+  float scale_log2;  // softmax_scale * log2(e)
+  int causal, has_window;
+  int64_t wl, wr;
+  const float* alibi;
+  int64_t al_sb, al_sh;
+  const void* mask;
+  int mask_dtype;
+  int64_t mk_sb, mk_sh, mk_si, mk_sj;
+  const uint8_t* bmap;
+  int64_t bm_sb, bm_sh;
+  int bm_cols;
+  int use_dropout;
+  uint32_t drop_thresh;  // drop when the Philox word < drop_thresh
+  float drop_scale;      // 1 / (1 - p)
+  uint32_t seed_lo, seed_hi, off_lo, off_hi;
+  const uint16_t* rope_cos;
+  const uint16_t* rope_sin;
+  int64_t rope_stride;
+};
+
+// Tile shape of one 16-bit kernel instantiation.
+struct Cfg16 {
+  int nw;  // wavefronts per workgroup
+  int qb;  // 32-row query blocks per wavefront
+  int bn;  // keys per K/V tile
+};
+
+__device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx) {
+  switch (dtype) {
+    case TRINIX_F32: return ((const float*)base)[idx];
+    case TRINIX_F16: return (float)((const _Float16*)base)[idx];
+    case TRINIX_BF16: return __uint_as_float(((uint32_t)((const uint16_t*)base)[idx]) << 16);
+    default: return (float)((const uint8_t*)base)[idx];
+  }
+}
+
+// Dropout on keys j0..j0+3 of row i: p <- keep ? p/(1-p) : 0.  Counter
+// (j0/4, i, b*H+h, offset_lo), key (seed_lo ^ offset_hi, seed_hi); word e
+// decides key j0+e.
+__device__ inline void dropout_group(float* x, const FwdParams& p, int bh, int i, int j0) {
+  const u32x4_t c = {(uint32_t)(j0 >> 2), (uint32_t)i, (uint32_t)bh, p.off_lo};
+  const u32x4_t rr = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) x[e] = (rr[e] < p.drop_thresh) ? 0.f : x[e] * p.drop_scale;
+}
+
+// Combine a value with the one held by lane l ^ 32 (v_permlane32_swap).
+__device__ inline float xlane_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float xlane_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wave-uniform "any lane" vote.
+__device__ inline bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
+
+// Launchers of the 16-bit kernels, one translation unit per (dtype, D).
+// Return hipErrorInvalidValue for a (cfg, features) pair not instantiated.
+hipError_t launch_attn16_bf16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
+hipError_t launch_attn16_bf16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
+hipError_t launch_attn16_f16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
+hipError_t launch_attn16_f16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
+
+// Feature bits of a launch (compile-time flags of the 16-bit kernels).
+enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4 };
+
+}  // namespace trinix

@@ -32,6 +32,11 @@ struct BF16 {
   __device__ static inline uint32_t pack(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
   }
+  // acc + lo(w) + hi(w) (v_dot2_f32_bf16 against (1, 1))
+  __device__ static inline float dot2_ones(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, 0x3f803f80u),
+                                           acc, false);
+  }
   __device__ static inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
@@ -43,6 +48,10 @@ struct F16 {
   __device__ static inline float hi(uint32_t w) { return (float)__builtin_bit_cast(f16x2_t, w)[1]; }
   __device__ static inline uint32_t pack(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, f16x2_t));
+  }
+  // acc + lo(w) + hi(w) (v_dot2_f32_f16 against (1, 1))
+  __device__ static inline float dot2_ones(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), __builtin_bit_cast(f16x2_t, 0x3c003c00u), acc, false);
   }
   __device__ static inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),

@@ -20,6 +20,9 @@ __global__ __launch_bounds__(256) void rope16_kernel(const uint16_t* x, int64_t 
                                                      int S, int H, int D, const uint16_t* cosp,
                                                      const uint16_t* sinp, int64_t cs, const int64_t* pos,
                                                      int64_t total) {
+  // One rounding per product and per sum, as eager PyTorch: no contraction
+  // of x*c - y*s into an fma (which would drop the rounding of one product).
+#pragma clang fp contract(off)
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= total) return;
   const int nch = D / 16;  // chunks of 8 in the first half
@@ -75,11 +78,13 @@ struct F32Scalar {
 // eager PyTorch's separate mul / add kernels.
 template <class S>
 __device__ inline float rope_lo(float a, float b, float c, float s) {
-  return S::rnd(__fsub_rn(S::rnd(__fmul_rn(a, c)), S::rnd(__fmul_rn(b, s))));
+#pragma clang fp contract(off)
+  return S::rnd(S::rnd(a * c) - S::rnd(b * s));
 }
 template <class S>
 __device__ inline float rope_hi(float a, float b, float c, float s) {
-  return S::rnd(__fadd_rn(S::rnd(__fmul_rn(b, c)), S::rnd(__fmul_rn(a, s))));
+#pragma clang fp contract(off)
+  return S::rnd(S::rnd(b * c) + S::rnd(a * s));
 }
 
 template <class S, class T>
