@@ -273,17 +273,17 @@ int check_tensor(const void* ptr, const int64_t st[4], int esize) {
 }
 
 // Tile configuration of the 16-bit kernel: 4 wavefronts x 32 query rows,
-// 64-key tiles.  TRINIX_ATTN_CFG="nw,qb,bn" overrides the choice (tuning
+// 64-key tiles, 2 wavefronts per SIMD.  TRINIX_ATTN_CFG="nw,occ,bn" overrides the choice (tuning
 // only; a configuration that is not built is rejected with
 // TRINIX_ERR_BAD_ARGUMENT).
 Cfg16 pick_cfg16(int64_t batch, int64_t hq, int64_t sq) {
-  Cfg16 c{4, 1, 64};
+  Cfg16 c{4, 2, 64};
   (void)batch;
   (void)hq;
   (void)sq;
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
-    int nw = 0, qb = 0, bn = 0;
-    if (sscanf(env, "%d,%d,%d", &nw, &qb, &bn) == 3) c = Cfg16{nw, qb, bn};
+    int nw = 0, occ = 0, bn = 0;
+    if (sscanf(env, "%d,%d,%d", &nw, &occ, &bn) == 3) c = Cfg16{nw, occ, bn};
   }
   return c;
 }
@@ -324,7 +324,7 @@ int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* ou
   if (head_dim != 64 && head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
   if (dtype == TRINIX_BF16 || dtype == TRINIX_F16) {
     const Cfg16 c = pick_cfg16(1 << 20, 1, 1 << 20);  // large-problem choice
-    out->block_m = 32 * c.nw * c.qb;
+    out->block_m = 32 * c.nw;
     out->block_n = c.bn;
     out->block_d = (int32_t)head_dim;
     out->waves = c.nw;
@@ -384,7 +384,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.G = p.Hq / p.Hkv;
   const bool f32 = a->dtype == TRINIX_F32;
   const Cfg16 cfg = pick_cfg16(a->batch, a->nheads_q, a->seqlen_q);
-  const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw * cfg.qb;
+  const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw;
   p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
   const int64_t total = (int64_t)p.B * p.Hq * p.num_mblk;
   if (total >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;

@@ -8,53 +8,88 @@
 // base.py:394-397): softmax first, then dropout, then PV.
 //
 // Decomposition: a workgroup of NW wavefronts owns one (batch, q-head,
-// NW*32*QB query rows); each wavefront owns QB blocks of 32 rows.  Per K/V
-// tile of BN keys a wavefront computes S^T = K Q^T with keys on the MFMA rows
-// and its queries on the columns, so each lane owns one query row of a block
-// (row max / sum: one lane^32 exchange).  O^T = V^T P^T takes P^T straight
-// from the S^T registers as the B operand; V sits transposed in LDS for the
-// A operand.  K/V fragments read from LDS are reused for all QB blocks.
-// K/V tiles are double-buffered in LDS: the global loads of tile t+1 are in
-// flight while tile t is computed, with one barrier per tile.
+// 32*NW query rows); each wavefront owns 32 rows.  Per K/V tile of BN keys a
+// wavefront computes S^T = K Q^T with keys on the MFMA rows and its queries
+// on the columns, so each lane owns one query row (row max / sum: one
+// lane^32 exchange).  O^T = V^T P^T takes P^T straight from the S^T
+// registers as the B operand; the V^T A operand is read from the row-major V
+// tile with the LDS transpose read ds_read_b64_tr_b16.
+//
+// Memory pipeline: K and V tiles go global -> LDS directly
+// (global_load_lds_dwordx4, no staging registers), K one tile ahead of V,
+// each in two LDS buffers.  Iteration t (one barrier):
+//     wait for K[t+1], V[t] ; barrier ; issue loads K[t+2], V[t+1]
+//     S[t+1] = K[t+1] Q^T          (MFMA)   } independent: the VALU softmax
+//     P[t]   = softmax(S[t])       (VALU)   } overlaps the QK MFMAs
+//     O     += V[t]^T P[t]         (MFMA)
+// LDS tiles are row-major with 16-byte units XOR-swizzled per row so the
+// MFMA operand reads are bank-conflict free.
 //
 // Tiles split into "full" tiles (every (i, j) of the workgroup allowed: no
 // per-element predicate) and "edge" tiles (causal diagonal, window borders,
-// the Sk tail); each kind runs its own straight-line loop body.  Edge tiles
-// that a wavefront's rows cannot see at all are skipped by that wavefront.
+// the Sk tail); each kind runs its own straight-line loop body.  Tiles a
+// wavefront's rows cannot see at all are skipped by that wavefront.
 //
-// Softmax details: scores stay in log2 units (scale * log2 e folded into one
-// FMA before v_exp_f32); the running max is only raised when the new tile
-// max exceeds it by more than TAU = 8 (then O and l are rescaled), so most
-// tiles skip the O rescale; p <= 2^TAU is exact enough in fp32 and in the
-// 16-bit P operand.
+// Softmax: scores stay in log2 units (scale * log2 e folded into one FMA
+// before v_exp_f32); the running max is raised only when a tile's max
+// exceeds it by more than TAU = 8 (then O and l are rescaled), so most tiles
+// skip the O rescale; p <= 2^TAU is exact enough in fp32 and in the 16-bit P
+// operand.  The row sum adds the rounded P that the PV product uses.
 #pragma once
+#include <climits>
 #include <type_traits>
 
 #include "attn_params.h"
 
 namespace trinix {
 
-template <class E, int D, int BN, int NW, int QB, bool ALIBI, bool MASK, bool DROP>
-__global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void attn_fwd_mfma16(const FwdParams p) {
-  constexpr int NT = NW * 64;
-  constexpr int WR = 32 * QB;  // query rows per wavefront
-  constexpr int BM = NW * WR;  // query rows per workgroup
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+
+// Swizzle of the 16-byte units of a D-wide row-major tile row.  K rows are
+// read 16 bytes per lane, 16 consecutive rows per access; V rows are read 8
+// bytes per lane by ds_read_b64_tr_b16, 4 consecutive rows x 64 bytes per
+// 32 lanes.
+template <int D>
+__device__ inline int swz_k(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int D>
+__device__ inline int swz_v(int row) {
+  return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
+}
+
+template <class E, int D, int BN, int NW, int OCC, bool ALIBI, bool MASK, bool DROP>
+__global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
+  constexpr int BM = NW * 32;  // query rows per workgroup
   constexpr int DS = D / 16;   // MFMA k-steps over head_dim (QK^T)
   constexpr int NB = BN / 32;  // 32-key blocks per tile
   constexpr int DB = D / 32;   // 32-wide head_dim blocks of O^T
-  constexpr int KCH = BN * D / 8;
-  constexpr int KPT = (KCH + NT - 1) / NT;
-  constexpr int VBLK = BN * D / 32;
-  constexpr int VPT = (VBLK + NT - 1) / NT;
+  constexpr int UPR = D / 8;   // 16-byte units per row
+  constexpr int TILE_UNITS = BN * UPR;
+  constexpr int LPW = TILE_UNITS / (64 * NW);  // direct loads per wavefront per tile (K or V)
   constexpr float TAU = 8.f;
-  static_assert(D % 64 == 0 && BN % 64 == 0, "tile shape");
+  static_assert(D % 64 == 0 && BN % 64 == 0 && TILE_UNITS % (64 * NW) == 0, "tile shape");
 
-  // K tile: row-major [key][D], 16-byte units XOR-swizzled by (key & 7).
-  // V tile: transposed [d][BN]; in each 16-key chunk key 8a+4g+e is stored
-  // at position 8g+4a+e, so one 16-byte read returns the 8 keys a lane of
-  // k-group g feeds to the PV MFMA; units XOR-swizzled by (d & 7).
-  __shared__ __attribute__((aligned(16))) uint16_t lds_k[2][BN * D];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_v[2][D * BN];
+  // Four separate LDS objects (not one array indexed by parity) so that the
+  // compiler can tell the buffer being read from the one an asynchronous
+  // global->LDS load is filling, and does not wait for that load.
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k0[BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[BN * D];
+  // Tile t lives in buffer slot (t - t_lo) & 1 of K and of V.  `slot` is a
+  // std::integral_constant in the full-tile loop (static buffer choice) and
+  // an int in the edge loops.
+  auto kbuf = [&](auto slot) __attribute__((always_inline)) -> uint16_t* {
+    if constexpr (std::is_integral_v<decltype(slot)>) return slot ? lds_k1 : lds_k0;
+    else return decltype(slot)::value ? lds_k1 : lds_k0;
+  };
+  auto vbuf = [&](auto slot) __attribute__((always_inline)) -> uint16_t* {
+    if constexpr (std::is_integral_v<decltype(slot)>) return slot ? lds_v1 : lds_v0;
+    else return decltype(slot)::value ? lds_v1 : lds_v0;
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 31, g = lane >> 5;
@@ -71,8 +106,10 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void attn_fwd_mfma16(cons
   const int hq = hkv * p.G + gq;
   const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
   const int m0 = mblk * BM;
-  const int iw0 = m0 + wave * WR;
-  const int iwl = min(iw0 + WR - 1, p.Sq - 1);
+  const int iw0 = m0 + wave * 32;
+  const int iwl = min(iw0 + 31, p.Sq - 1);
+  const int i = iw0 + r;
+  const int ic = min(i, p.Sq - 1);
   const bool wave_live = iw0 < p.Sq;
 
   // Key tiles the workgroup visits, and the sub-range of full tiles.
@@ -96,14 +133,12 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void attn_fwd_mfma16(cons
   t_fhi = min(max(t_fhi, t_flo), t_hi);
   if (!(p.scale_log2 > 0.f)) t_flo = t_fhi = t_hi;  // raw-max trick needs scale > 0
 
-  // Q rows in registers: qr[qb][ds] = q[i][ds*16 + g*8 .. +8], i = iw0+32qb+r.
-  u32x4_t qr[QB][DS];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int ic = min(iw0 + qb * 32 + r, p.Sq - 1);
+  // Q row in registers: qr[ds] = q[i][ds*16 + g*8 .. +8].
+  u32x4_t qr[DS];
+  {
     const uint16_t* qrow = p.q + b * p.q_sb + hq * p.q_sh + (int64_t)ic * p.q_ss;
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) qr[qb][ds] = *(const u32x4_t*)(qrow + ds * 16 + g * 8);
+    for (int ds = 0; ds < DS; ++ds) qr[ds] = *(const u32x4_t*)(qrow + ds * 16 + g * 8);
     if (p.rope_cos) {
 #pragma clang fp contract(off)
       // Fused RoPE (reference trinix/layers/embeddings/rope.py:111-118):
@@ -116,7 +151,7 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void attn_fwd_mfma16(cons
       for (int ds = 0; ds < DS / 2; ++ds) {
         const u32x4_t cw = *(const u32x4_t*)(crow + ds * 16 + g * 8);
         const u32x4_t sw = *(const u32x4_t*)(srow + ds * 16 + g * 8);
-        u32x4_t x1 = qr[qb][ds], x2 = qr[qb][ds + DS / 2];
+        u32x4_t x1 = qr[ds], x2 = qr[ds + DS / 2];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float c0 = E::lo(cw[e]), c1 = E::hi(cw[e]);
@@ -130,321 +165,325 @@ __global__ __launch_bounds__(NW * 64, QB == 1 ? 2 : 1) void attn_fwd_mfma16(cons
           x1[e] = E::pack(lo0, lo1);
           x2[e] = E::pack(hi0, hi1);
         }
-        qr[qb][ds] = x1;
-        qr[qb][ds + DS / 2] = x2;
+        qr[ds] = x1;
+        qr[ds + DS / 2] = x2;
       }
     }
   }
 
-  f32x16_t acc[QB][DB];
-  float m_run[QB], l_run[QB];
+  f32x16_t acc[DB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m_run[qb] = -INFINITY;
-    l_run[qb] = 0.f;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) acc[qb][db] = (f32x16_t){};
-  }
+  for (int db = 0; db < DB; ++db) acc[db] = (f32x16_t){};
+  float m_run = -INFINITY, l_run = 0.f;
   const float c = p.scale_log2;
+  // Allowed keys of this row: jlo <= j <= jhi (empty if jlo > jhi), from
+  // j < Sk, causal j <= i and window -wl <= j - i <= wr (clamped to int32).
+  int jlo = 0, jhi = p.Sk - 1;
+  if (p.causal) jhi = min(jhi, i);
+  if (p.has_window) {
+    jlo = (int)max((int64_t)jlo, (int64_t)i - p.wl);
+    jhi = (int)min((int64_t)jhi, (int64_t)i + p.wr);
+  }
+  const uint32_t jspan = jhi >= jlo ? (uint32_t)(jhi - jlo) : 0u;
+  if (jhi < jlo) jlo = INT_MAX;  // no allowed key: (j - jlo) wraps past jspan for every j
   float slope_l2 = 0.f;
   if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
-  const char* mrow[QB];
+  const char* mrow = nullptr;
   if constexpr (MASK) {
     const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int ic = min(iw0 + qb * 32 + r, p.Sq - 1);
-      mrow[qb] = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)ic * p.mk_si) * esz;
-    }
+    mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)ic * p.mk_si) * esz;
   }
 
+  // ---- direct global -> LDS tile loads --------------------------------
+  // Load l of this wavefront fills LDS units [64*(wave*LPW + l), +64) of the
+  // tile (one per lane); unit u holds key row u / UPR, physical unit u % UPR,
+  // i.e. logical 16-byte unit (u % UPR) ^ swz(row) of that row.
   const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  u32x4_t kst[KPT];
-  u32x4_t vst[VPT][4];
-
-  auto gload = [&](int tile) {
+  int ld_key[LPW], ld_kunit[LPW], ld_vunit[LPW];
+#pragma unroll
+  for (int l = 0; l < LPW; ++l) {
+    const int u = (wave * LPW + l) * 64 + lane;
+    ld_key[l] = u / UPR;
+    ld_kunit[l] = (u % UPR) ^ swz_k<D>(ld_key[l]);
+    ld_vunit[l] = (u % UPR) ^ swz_v<D>(ld_key[l]);
+  }
+  // Rows past Sk are loaded from row Sk-1 (finite data): their scores are
+  // masked to -inf and their P is 0, so they never contribute.
+  auto load_tile = [&](const uint16_t* base, int64_t ss, const int* units, uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
     const int n0 = tile * BN;
 #pragma unroll
-    for (int t = 0; t < KPT; ++t) {
-      const int cidx = tid + t * NT;
-      if (cidx < KCH) {
-        const int key = cidx / (D / 8), unit = cidx % (D / 8);
-        const int j = n0 + key;
-        kst[t] = j < p.Sk ? *(const u32x4_t*)(kbase + (int64_t)j * p.k_ss + unit * 8) : (u32x4_t){};
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < VPT; ++t) {
-      const int blk = tid + t * NT;
-      if (blk < VBLK) {
-        const int kg = blk % (BN / 4), dch = blk / (BN / 4);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int j = n0 + kg * 4 + rr;
-          vst[t][rr] = j < p.Sk ? *(const u32x4_t*)(vbase + (int64_t)j * p.v_ss + dch * 8) : (u32x4_t){};
-        }
-      }
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int t = 0; t < KPT; ++t) {
-      const int cidx = tid + t * NT;
-      if (cidx < KCH) {
-        const int key = cidx / (D / 8), unit = cidx % (D / 8);
-        *(u32x4_t*)(&lds_k[buf][key * D + ((unit ^ (key & 7)) * 8)]) = kst[t];
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < VPT; ++t) {
-      const int blk = tid + t * NT;
-      if (blk < VBLK) {
-        const int kg = blk % (BN / 4), dch = blk / (BN / 4);
-        const int c16 = kg >> 2, a = (kg >> 1) & 1, gg = kg & 1;
-#pragma unroll
-        for (int dd = 0; dd < 8; ++dd) {
-          const uint32_t sel = (dd & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t w0 = __builtin_amdgcn_perm(vst[t][1][dd >> 1], vst[t][0][dd >> 1], sel);
-          const uint32_t w1 = __builtin_amdgcn_perm(vst[t][3][dd >> 1], vst[t][2][dd >> 1], sel);
-          const int d = dch * 8 + dd;
-          const int unit = (2 * c16 + gg) ^ (d & 7);
-          *(u32x2_t*)(&lds_v[buf][d * BN + unit * 8 + a * 4]) = (u32x2_t){w0, w1};
-        }
-      }
+    for (int l = 0; l < LPW; ++l) {
+      const int j = min(n0 + ld_key[l], p.Sk - 1);
+      const uint16_t* src = base + (int64_t)j * ss + units[l] * 8;
+      lds_void_t* dst = (lds_void_t*)((char*)lds_tile + (wave * LPW + l) * 1024);
+      __builtin_amdgcn_global_load_lds((const void*)src, dst, 16, 0, 0);
     }
   };
 
-  // One tile: S = QK^T, softmax update, O += PV.  PRED: per-element
-  // causal/window/bounds predicate needed; MCODE (MASK only): 0 = mask
-  // block all zero (not read), 1 = read the mask.
-  auto compute = [&](auto pred_c, int buf, int n0, int mcode) {
-    constexpr bool PRED = decltype(pred_c)::value;
-    constexpr bool GENERIC = PRED || ALIBI || MASK;
-    f32x16_t s[QB][NB];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) s[qb][nb] = (f32x16_t){};
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int row = nb * 32 + r;
-#pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const int unit = (ds * 2 + g) ^ (row & 7);
-        const u32x4_t a = *(const u32x4_t*)(&lds_k[buf][row * D + unit * 8]);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[qb][nb] = E::mfma(a, qr[qb][ds], s[qb][nb]);
-      }
-    }
-    u32x4_t pb[QB][NB][2];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int i = iw0 + qb * 32 + r;
-      float mx = -INFINITY;
-      if constexpr (GENERIC) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int vq = 0; vq < 4; ++vq) {
-            const int j0 = n0 + nb * 32 + vq * 8 + g * 4;
-            float mv[4] = {0.f, 0.f, 0.f, 0.f};
-            if constexpr (MASK) {
-              if (mcode) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  if (j0 + e < p.Sk) mv[e] = load_mask_elem(mrow[qb], p.mask_dtype, (int64_t)(j0 + e) * p.mk_sj);
-              }
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int j = j0 + e;
-              float x = s[qb][nb][vq * 4 + e] * c;
-              if constexpr (ALIBI) x += slope_l2 * (float)abs(i - j);
-              if constexpr (MASK) x += mv[e] * kLog2e;
-              if constexpr (PRED) {
-                bool ok = j < p.Sk;
-                if (p.causal) ok = ok && (j <= i);
-                if (p.has_window) {
-                  const int64_t dj = (int64_t)j - i;
-                  ok = ok && (dj >= -p.wl) && (dj <= p.wr);
-                }
-                x = ok ? x : -INFINITY;
-              }
-              s[qb][nb][vq * 4 + e] = x;
-              mx = fmaxf(mx, x);
-            }
-          }
-        mx = xlane_max(mx);
-      } else {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[qb][nb][v]);
-        mx = xlane_max(mx) * c;  // raw max scaled: c > 0 on this path
-      }
-      // Lazy rescale: keep the running max unless this tile exceeds it by TAU.
-      if (__builtin_expect(wave_any(mx > m_run[qb] + TAU), 0)) {
-        const float m_new = fmaxf(m_run[qb], mx);
-        // a row that has seen no allowed key yet (m_new = -inf; its acc and l
-        // are 0) keeps alpha finite instead of exp2(-inf - -inf) = NaN
-        const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-        l_run[qb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db) acc[qb][db] *= alpha;
-        m_run[qb] = m_new;
-      }
-      if constexpr (GENERIC) {
-        const float m_use = m_run[qb] == -INFINITY ? 0.f : m_run[qb];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) s[qb][nb][v] = __builtin_amdgcn_exp2f(s[qb][nb][v] - m_use);
-      } else {
-        const float mneg = -m_run[qb];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) s[qb][nb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qb][nb][v], c, mneg));
-      }
-      if constexpr (DROP) {
-        // l sums the probabilities before dropout (eager: softmax, then dropout)
-        float rs = 0.f;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) rs += s[qb][nb][v];
-        l_run[qb] += rs;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int vq = 0; vq < 4; ++vq) {
-            float x[4] = {s[qb][nb][vq * 4 + 0], s[qb][nb][vq * 4 + 1], s[qb][nb][vq * 4 + 2],
-                          s[qb][nb][vq * 4 + 3]};
-            dropout_group(x, p, b * p.Hq + hq, i, n0 + nb * 32 + vq * 8 + g * 4);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) s[qb][nb][vq * 4 + e] = x[e];
-          }
-      }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          pb[qb][nb][kk] = (u32x4_t){E::pack(s[qb][nb][kk * 8 + 0], s[qb][nb][kk * 8 + 1]),
-                                     E::pack(s[qb][nb][kk * 8 + 2], s[qb][nb][kk * 8 + 3]),
-                                     E::pack(s[qb][nb][kk * 8 + 4], s[qb][nb][kk * 8 + 5]),
-                                     E::pack(s[qb][nb][kk * 8 + 6], s[qb][nb][kk * 8 + 7])};
-      if constexpr (!DROP) {
-        // Row sum of the rounded P the PV product uses, two elements per
-        // v_dot2 (x.lo*1 + x.hi*1 + acc), four independent accumulators.
-        float r4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) r4[e] = E::dot2_ones(pb[qb][nb][kk][e], r4[e]);
-        l_run[qb] += (r4[0] + r4[1]) + (r4[2] + r4[3]);
-      }
-    }
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const int d = db * 32 + r;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int unit = (2 * (2 * nb + kk) + g) ^ (d & 7);
-          const u32x4_t a = *(const u32x4_t*)(&lds_v[buf][d * BN + unit * 8]);
-#pragma unroll
-          for (int qb = 0; qb < QB; ++qb) acc[qb][db] = E::mfma(a, pb[qb][nb][kk], acc[qb][db]);
-        }
-    }
-  };
-
-  // Mask block-map code of this wavefront for the tile at n0 (MASK only):
-  // -1 = every block of the wavefront's rows is all -inf (skip), 0 = all
-  // zero (no load), 1 = load the mask.
-  auto mask_code = [&](int n0) -> int {
+  // ---- per-tile pieces ---------------------------------------------------
+  auto mask_code = [&](int n0) __attribute__((always_inline)) -> int {
     if (!p.bmap) return 1;
+    const uint8_t* bm = p.bmap + b * p.bm_sb + hq * p.bm_sh + (int64_t)(iw0 / 32) * p.bm_cols;
     bool all_skip = true, any_other = false;
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      const int rb = (iw0 + qb * 32) / 32;
-      if (iw0 + qb * 32 >= p.Sq) continue;
-      const uint8_t* bm = p.bmap + b * p.bm_sb + hq * p.bm_sh + (int64_t)rb * p.bm_cols;
-#pragma unroll
-      for (int cb = 0; cb < BN / 64; ++cb) {
-        if (n0 + cb * 64 >= p.Sk) break;  // past the last block-map column
-        const uint8_t code = bm[n0 / 64 + cb];
-        all_skip = all_skip && code == 2;
-        any_other = any_other || code != 0;
-      }
+    for (int cb = 0; cb < BN / 64; ++cb) {
+      if (n0 + cb * 64 >= p.Sk) break;  // past the last block-map column
+      const uint8_t code = bm[n0 / 64 + cb];
+      all_skip = all_skip && code == 2;
+      any_other = any_other || code != 0;
     }
     return all_skip ? -1 : (any_other ? 1 : 0);
   };
 
-  auto step = [&](auto pred_c, int t, int buf) {
-    constexpr bool PRED = decltype(pred_c)::value;
-    lstore(buf);
-    __syncthreads();
-    if (t + 1 < t_hi) gload(t + 1);
-    const int n0 = t * BN;
-    bool live = wave_live;
-    if constexpr (PRED) {
-      if (p.causal && n0 > iwl) live = false;
-      if (p.has_window && ((int64_t)n0 - iwl > p.wr || (int64_t)n0 + BN - 1 - iw0 < -p.wl)) live = false;
-    }
-    int mcode = 0;
-    if constexpr (MASK) {
-      if (live) {
-        mcode = mask_code(n0);
-        if (mcode < 0) live = false;
+  // S^T = K Q^T for one tile (keys nb*32 + MFMA row, queries on columns).
+  auto qk = [&](const uint16_t* kt, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      s[nb] = (f32x16_t){};
+      const int row = nb * 32 + r;
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const int unit = (ds * 2 + g) ^ swz_k<D>(row);
+        const u32x4_t a = *(const u32x4_t*)(kt + row * D + unit * 8);
+        s[nb] = E::mfma(a, qr[ds], s[nb]);
       }
     }
-    if (live) compute(pred_c, buf, n0, mcode);
   };
 
-  if (t_lo < t_hi) gload(t_lo);
-  int t = t_lo, buf = 0;
-  for (; t < t_flo; ++t, buf ^= 1) step(std::true_type{}, t, buf);
-  for (; t < t_fhi; ++t, buf ^= 1) step(std::false_type{}, t, buf);
-  for (; t < t_hi; ++t, buf ^= 1) step(std::true_type{}, t, buf);
+  // O^T += V^T P^T: the A operand (8 keys of one head_dim row per lane) comes
+  // from two transpose reads of the row-major V tile.  16-lane group G of the
+  // wavefront covers head_dim d0 + 0..15 (d0 = db*32 + 16*(G&1)) for k-group
+  // g = G>>1; lane s of the group addresses 4 consecutive d (d0 + 4*(s&3))
+  // at key row kb + 4g + s/4 (+8 for the second read) and receives the 4
+  // keys kb + 4g + 0..3 of head_dim d0 + s.
+  const int tr_G = lane >> 4, tr_s = lane & 15;
+  const int tr_g = tr_G >> 1, tr_dh = tr_G & 1;
+  auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);  // logical unit of d0 + 4*(s&3)
+      const int half = (tr_s & 1) * 4;                        // element offset in the unit
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
+          const int row1 = row0 + 8;
+          const s16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t*)(vt + row0 * D + ((u ^ swz_v<D>(row0)) * 8) + half));
+          const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_s16x4_t*)(vt + row1 * D + ((u ^ swz_v<D>(row1)) * 8) + half));
+          const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
+          const u32x4_t a = {l2[0], l2[1], h2[0], h2[1]};
+          acc[db] = E::mfma(a, pb[nb][kk], acc[db]);
+        }
+    }
+  };
+
+  // Softmax update of one tile; writes P^T packed as the PV B operand.
+  // GENERIC (edge tile, ALiBi or mask): x = s*c + bias (or -inf where not
+  // allowed); plain full tiles keep raw scores, take the max of the raw
+  // scores (c > 0) and fold the scale into one FMA before the exp.
+  auto softmax = [&](auto pred_c, f32x16_t(&s)[NB], int n0, int mcode, u32x4_t(&pb)[NB][2])
+                     __attribute__((always_inline)) {
+    constexpr bool PRED = decltype(pred_c)::value;
+    constexpr bool GENERIC = PRED || ALIBI || MASK;
+    float mx = -INFINITY;
+    if constexpr (GENERIC) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int j0 = n0 + nb * 32 + vq * 8 + g * 4;
+          float mv[4] = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (MASK) {
+            if (mcode > 0) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (j0 + e < p.Sk) mv[e] = load_mask_elem(mrow, p.mask_dtype, (int64_t)(j0 + e) * p.mk_sj);
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = j0 + e;
+            float x = s[nb][vq * 4 + e] * c;
+            if constexpr (ALIBI) x += slope_l2 * (float)abs(i - j);
+            if constexpr (MASK) x += mv[e] * kLog2e;
+            if constexpr (PRED) x = (uint32_t)(j - jlo) <= jspan ? x : -INFINITY;
+            s[nb][vq * 4 + e] = x;
+            mx = fmaxf(mx, x);
+          }
+        }
+      mx = xlane_max(mx);
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[nb][v]);
+      mx = xlane_max(mx) * c;  // raw max scaled: c > 0 on this path
+    }
+    // Lazy rescale: keep the running max unless this tile exceeds it by TAU.
+    if (__builtin_expect(wave_any(mx > m_run + TAU), 0)) {
+      const float m_new = fmaxf(m_run, mx);
+      // a row that has seen no allowed key yet (m_new = -inf; its acc and l
+      // are 0) keeps alpha finite instead of exp2(-inf - -inf) = NaN
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+      m_run = m_new;
+    }
+    if constexpr (GENERIC) {
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(s[nb][v] - m_use);
+    } else {
+      const float mneg = -m_run;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][v], c, mneg));
+    }
+    if constexpr (DROP) {
+      // l sums the probabilities before dropout (eager: softmax, then dropout)
+      float rs = 0.f;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) rs += s[nb][v];
+      l_run += rs;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          float x[4] = {s[nb][vq * 4 + 0], s[nb][vq * 4 + 1], s[nb][vq * 4 + 2], s[nb][vq * 4 + 3]};
+          dropout_group(x, p, b * p.Hq + hq, i, n0 + nb * 32 + vq * 8 + g * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = x[e];
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        pb[nb][kk] = (u32x4_t){E::pack(s[nb][kk * 8 + 0], s[nb][kk * 8 + 1]), E::pack(s[nb][kk * 8 + 2], s[nb][kk * 8 + 3]),
+                               E::pack(s[nb][kk * 8 + 4], s[nb][kk * 8 + 5]), E::pack(s[nb][kk * 8 + 6], s[nb][kk * 8 + 7])};
+    if constexpr (!DROP) {
+      // Row sum of the rounded P the PV product uses, two elements per
+      // v_dot2 (x.lo*1 + x.hi*1 + acc), four independent accumulators.
+      float r4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r4[e] = E::dot2_ones(pb[nb][kk][e], r4[e]);
+      l_run += (r4[0] + r4[1]) + (r4[2] + r4[3]);
+    }
+  };
+
+  // Whether tile `tile` has any allowed (i, j) for this wavefront's rows.
+  auto tile_live = [&](int tile) __attribute__((always_inline)) -> bool {
+    if (!wave_live) return false;
+    const int n0 = tile * BN;
+    if (p.causal && n0 > iwl) return false;
+    if (p.has_window && ((int64_t)n0 - iwl > p.wr || (int64_t)n0 + BN - 1 - iw0 < -p.wl)) return false;
+    return true;
+  };
+
+  // ---- main loop -----------------------------------------------------------
+  // One iteration for tile t (buffer slot `slot` of t): S[t] is in `sc`
+  // (valid if live_c); S[t+1] is computed into `sn`.
+  auto step = [&](auto pred_c, auto slot, int t, f32x16_t(&sc)[NB], f32x16_t(&sn)[NB], bool live_c)
+                  __attribute__((always_inline)) -> bool {
+    auto other = [&]() {
+      if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
+      else return std::integral_constant<int, 1 - decltype(slot)::value>{};
+    }();
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t+1], V[t] landed
+    __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
+    if (t + 2 < t_hi) load_tile(kbase, p.k_ss, ld_kunit, kbuf(slot), t + 2);
+    if (t + 1 < t_hi) load_tile(vbase, p.v_ss, ld_vunit, vbuf(other), t + 1);
+    const bool live_n = t + 1 < t_hi && tile_live(t + 1);
+    if (live_n) qk(kbuf(other), sn);
+    if (live_c) {
+      const int n0 = t * BN;
+      int mcode = 1;
+      if constexpr (MASK) mcode = mask_code(n0);
+      if (mcode >= 0) {
+        u32x4_t pb[NB][2];
+        softmax(pred_c, sc, n0, mcode, pb);
+        pv(vbuf(slot), pb);
+      }
+    }
+    return live_n;
+  };
+  f32x16_t sa[NB], sb[NB];
+  bool live_a = false;
+  if (t_lo < t_hi) {
+    load_tile(kbase, p.k_ss, ld_kunit, kbuf(std::integral_constant<int, 0>{}), t_lo);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    live_a = tile_live(t_lo);
+    if (live_a) qk(kbuf(std::integral_constant<int, 0>{}), sa);
+    if (t_lo + 1 < t_hi) load_tile(kbase, p.k_ss, ld_kunit, kbuf(std::integral_constant<int, 1>{}), t_lo + 1);
+    load_tile(vbase, p.v_ss, ld_vunit, vbuf(std::integral_constant<int, 0>{}), t_lo);
+  }
+  // Full tiles run in pairs starting at an even offset from t_lo, so the
+  // buffer slots are static and S[t] / S[t+1] alternate between sa and sb
+  // without register copies (the full range is trimmed to start at an even
+  // offset and to an even length; trimmed tiles run as edge tiles, which are
+  // always exact).  Edge tiles run one at a time and copy S[t+1] into sa.
+  auto edge_range = [&](int& t, int end) __attribute__((always_inline)) {
+    for (; t < end; ++t) {
+      const bool live_b = step(std::true_type{}, (t - t_lo) & 1, t, sa, sb, live_a);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) sa[nb] = sb[nb];
+      live_a = live_b;
+    }
+  };
+  if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
+  t_fhi -= (t_fhi - t_flo) & 1;
+  int t = t_lo;
+  edge_range(t, t_flo);
+  for (; t < t_fhi; t += 2) {
+    const bool live_b = step(std::false_type{}, std::integral_constant<int, 0>{}, t, sa, sb, live_a);
+    live_a = step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1, sb, sa, live_b);
+  }
+  edge_range(t, t_hi);
 
   // Epilogue: O = acc / l (NaN for rows with no allowed key, like the eager
   // softmax over an all -inf row), optional log-sum-exp.
+  const float l = xlane_sum(l_run);
+  if (i < p.Sq) {
+    const float inv = 1.f / l;
+    uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)i * p.o_ss;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    const int i = iw0 + qb * 32 + r;
-    const float l = xlane_sum(l_run[qb]);
-    if (i < p.Sq) {
-      const float inv = 1.f / l;
-      uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)i * p.o_ss;
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-          const int d0 = db * 32 + vq * 8 + g * 4;
-          const u32x2_t w2 = {E::pack(acc[qb][db][vq * 4 + 0] * inv, acc[qb][db][vq * 4 + 1] * inv),
-                              E::pack(acc[qb][db][vq * 4 + 2] * inv, acc[qb][db][vq * 4 + 3] * inv)};
-          *(u32x2_t*)(orow + d0) = w2;
-        }
-      if (p.lse && g == 0) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = (m_run[qb] + __log2f(l)) * kLn2;
-    }
+      for (int vq = 0; vq < 4; ++vq) {
+        const int d0 = db * 32 + vq * 8 + g * 4;
+        const u32x2_t w2 = {E::pack(acc[db][vq * 4 + 0] * inv, acc[db][vq * 4 + 1] * inv),
+                            E::pack(acc[db][vq * 4 + 2] * inv, acc[db][vq * 4 + 3] * inv)};
+        *(u32x2_t*)(orow + d0) = w2;
+      }
+    if (p.lse && g == 0) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = (m_run + __log2f(l)) * kLn2;
   }
 }
 
-// Instantiates the launcher of one (dtype, D): the given tile configs for
-// every feature combination.
-template <class E, int D, int BN, int NW, int QB>
+// Launcher of one (dtype, D, tile shape): every feature combination.
+template <class E, int D, int BN, int NW, int OCC>
 hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   const dim3 grid((unsigned)p.total_work), block(NW * 64);
   switch (feat) {
-#define TRINIX_CASE(F)                                                                                         \
-  case F:                                                                                                      \
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, QB, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,       \
-                                        (F & kFeatDropout) != 0>),                                             \
-                       grid, block, 0, st, p);                                                                 \
+#define TRINIX_CASE(F)                                                                                          \
+  case F:                                                                                                       \
+    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,         \
+                                        (F & kFeatDropout) != 0>),                                              \
+                       grid, block, 0, st, p);                                                                  \
     return hipGetLastError();
     TRINIX_CASE(0)
     TRINIX_CASE(1)
@@ -459,25 +498,21 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   }
 }
 
-// A tile config without ALiBi / mask / dropout.
-template <class E, int D, int BN, int NW, int QB>
+// One tile shape without ALiBi / mask / dropout (tuning sweeps).
+template <class E, int D, int BN, int NW, int OCC>
 hipError_t launch_plain(const FwdParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, QB, false, false, false>), dim3((unsigned)p.total_work),
+  hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, false, false, false>), dim3((unsigned)p.total_work),
                      dim3(NW * 64), 0, st, p);
   return hipGetLastError();
 }
 
-// Tile configs built for every (dtype, D): (nw, qb, bn) = (4, 1, 64) with
-// all feature combinations; (4, 2, 64) and (4, 1, 128) without features
-// (kept for tuning sweeps).
-#define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                  \
-  hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {               \
-    if (cfg.bn == 64 && cfg.nw == 4 && cfg.qb == 1) return launch_feat<E, D, 64, 4, 1>(p, feat, st); \
-    if (feat == 0 && cfg.bn == 64 && cfg.nw == 4 && cfg.qb == 2)                            \
-      return launch_plain<E, D, 64, 4, 2>(p, st);                                           \
-    if (feat == 0 && cfg.bn == 128 && cfg.nw == 4 && cfg.qb == 1)                           \
-      return launch_plain<E, D, 128, 4, 1>(p, st);                                          \
-    return hipErrorInvalidValue;                                                            \
+// Tile configs built for every (dtype, D): (nw, occ, bn) = (4, 2, 64) with
+// every feature combination and (4, 1, 64) without features.
+#define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                              \
+  hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                           \
+    if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 2) return launch_feat<E, D, 64, 4, 2>(p, feat, st);  \
+    if (feat == 0 && cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 1) return launch_plain<E, D, 64, 4, 1>(p, st); \
+    return hipErrorInvalidValue;                                                                        \
   }
 
 }  // namespace trinix

@@ -40,9 +40,9 @@ struct FwdParams {
 
 // Tile shape of one 16-bit kernel instantiation.
 struct Cfg16 {
-  int nw;  // wavefronts per workgroup
-  int qb;  // 32-row query blocks per wavefront
-  int bn;  // keys per K/V tile
+  int nw;   // wavefronts per workgroup (32 query rows each)
+  int occ;  // target wavefronts per SIMD (register budget 512 / occ)
+  int bn;   // keys per K/V tile
 };
 
 __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx) {
