@@ -36,11 +36,38 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="c3")
-    ap.add_argument("--cpu-sample-heads", type=int, default=4,
+    ap.add_argument("--cpu-sample-heads", type=int, default=32,
                     help="query heads of batch 0 timed on the CPU oracle")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--all", action="store_true", help="also time every other workload (extra field)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (scale factor of the HBM byte counters)")
     return ap.parse_args()
+
+
+def traffic_from_profile(workload):
+    """HBM bytes per launch of the attention kernel, measured offline with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (scaled by a plain copy's
+    counters) and recorded in profiles/attn_fwd_<workload>_traffic.txt."""
+    path = os.path.join(ROOT, "profiles", f"attn_fwd_{workload}_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def calibrate_copy(torch):
+    n = 256 * 1024 * 1024 // 2
+    x = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read_per_launch": n * 2, "copy_bytes_written_per_launch": n * 2}), flush=True)
 
 
 def step_fn(w, inp, torch):
@@ -94,8 +121,15 @@ def measure(w, args, torch):
 
     inp = make_inputs(w, device="cuda")
     fn = step_fn(w, inp, torch)
-    for _ in range(args.warmup):
+    # W warm-up steps, extended until the GPU has been busy for ~0.3 s so the
+    # timed region runs at the steady-state clock (untimed).
+    t_warm = time.perf_counter()
+    n = 0
+    while n < args.warmup or time.perf_counter() - t_warm < 0.3:
         fn()
+        n += 1
+        if n % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -104,10 +138,20 @@ def measure(w, args, torch):
     ms = (time.perf_counter() - t0) * 1e3 / args.steps
     fl = flops(w)
     kfn = kernel_only_fn(w, inp, torch)
-    for _ in range(2):
+    for _ in range(3):
         kfn()
-    kms = time_events(kfn, max(args.steps, 10), torch)
+    kms = time_events(kfn, max(args.steps, 20), torch)
     return inp, fl, ms, kms
+
+
+def algo_bytes(w):
+    """Minimum HBM bytes of one launch: q, k, v read once, out written once
+    (+ the mask read once)."""
+    esz = 4 if str(w.dtype) == "torch.float32" else 2
+    n = (2 * w.batch * w.seqlen * w.nheads + 2 * w.batch * w.seqlen * w.nheads_kv) * w.head_dim * esz
+    if w.block_mask:
+        n += w.seqlen * w.seqlen * 4
+    return n
 
 
 def cpu_baseline(w, nheads, torch):
@@ -159,6 +203,9 @@ def main():
         sys.exit(2)
     import torch
 
+    if args.calibrate_copy:
+        calibrate_copy(torch)
+        return
     from trinix_amd.workloads import WORKLOADS
     from trinix_amd import _native
 
@@ -197,7 +244,9 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(k_tflops / peak, 4),
             "kernel_ms": round(kms, 4),
-            "traffic": None,
+            "traffic": traffic_from_profile(w.name),
+            "traffic_unit": "bytes/launch",
+            "algorithmic_bytes": algo_bytes(w),
         },
         "native_library": str(_native.LIB_PATH) if _native.library_loaded() else None,
     }
