@@ -6,7 +6,15 @@ their GPU work runs in hand-written HIP kernels (``libtrinix_attn.so``).
 """
 from .version import __version__
 from .kernels import TritonAttentionKernel, TritonRoPEKernel, calculate_attention_block_sizes
-from .layers.attention.functional import triton_attn_func
+from .layers.attention import (
+    FastBaseAttention,
+    FastGroupedQueryAttention,
+    FastMultiHeadAttention,
+    FastMultiHeadSelfAttention,
+    FastMultiQueryAttention,
+    triton_attn_func,
+)
+from .layers.embeddings import FastALiBiPositionEmbedding, FastRoPEPositionEmbedding
 
 __all__ = [
     "__version__",
@@ -14,4 +22,11 @@ __all__ = [
     "TritonRoPEKernel",
     "calculate_attention_block_sizes",
     "triton_attn_func",
+    "FastBaseAttention",
+    "FastGroupedQueryAttention",
+    "FastMultiHeadAttention",
+    "FastMultiHeadSelfAttention",
+    "FastMultiQueryAttention",
+    "FastRoPEPositionEmbedding",
+    "FastALiBiPositionEmbedding",
 ]
