@@ -16,14 +16,12 @@
 // tile with the LDS transpose read ds_read_b64_tr_b16.
 //
 // Memory pipeline: K and V tiles go global -> LDS directly
-// (global_load_lds_dwordx4, no staging registers), K one tile ahead of V,
-// each in two LDS buffers.  Iteration t (one barrier):
-//     wait for K[t+1], V[t] ; barrier ; issue loads K[t+2], V[t+1]
-//     S[t+1] = K[t+1] Q^T          (MFMA)   } independent: the VALU softmax
-//     P[t]   = softmax(S[t])       (VALU)   } overlaps the QK MFMAs
-//     O     += V[t]^T P[t]         (MFMA)
-// LDS tiles are row-major with 16-byte units XOR-swizzled per row so the
-// MFMA operand reads are bank-conflict free.
+// (global_load_lds_dwordx4, no staging registers) into two LDS buffers
+// each; the loads of tile t+1 are in flight while tile t is computed, with
+// one barrier per tile.  Within a tile the LDS operand reads run ahead of
+// their MFMAs (explicit prefetch, pinned with sched_group_barrier).  LDS
+// tiles are row-major with 16-byte units XOR-swizzled per row so the MFMA
+// operand reads are bank-conflict free.
 //
 // Tiles split into "full" tiles (every (i, j) of the workgroup allowed: no
 // per-element predicate) and "edge" tiles (causal diagonal, window borders,
@@ -237,17 +235,32 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
 
   // S^T = K Q^T for one tile (keys nb*32 + MFMA row, queries on columns).
+  // K fragments are read KPF MFMAs ahead; the sched_group_barriers keep the
+  // reads ahead of their MFMAs instead of letting each MFMA wait on its read.
+  constexpr int NQK = NB * DS;
+  constexpr int KPF = 3;
   auto qk = [&](const uint16_t* kt, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      s[nb] = (f32x16_t){};
+    auto kread = [&](int k) __attribute__((always_inline)) {
+      const int nb = k / DS, ds = k % DS;
       const int row = nb * 32 + r;
+      const int unit = (ds * 2 + g) ^ swz_k<D>(row);
+      return *(const u32x4_t*)(kt + row * D + unit * 8);
+    };
+    u32x4_t kf[NQK];
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) {
-        const int unit = (ds * 2 + g) ^ swz_k<D>(row);
-        const u32x4_t a = *(const u32x4_t*)(kt + row * D + unit * 8);
-        s[nb] = E::mfma(a, qr[ds], s[nb]);
-      }
+    for (int k = 0; k < KPF; ++k) kf[k] = kread(k);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) s[nb] = (f32x16_t){};
+#pragma unroll
+    for (int k = 0; k < NQK; ++k) {
+      if (k + KPF < NQK) kf[k + KPF] = kread(k + KPF);
+      s[k / DS] = E::mfma(kf[k], qr[k % DS], s[k / DS]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, KPF, 0);
+#pragma unroll
+    for (int k = 0; k < NQK; ++k) {
+      if (k + KPF < NQK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
   };
 
@@ -259,25 +272,35 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // keys kb + 4g + 0..3 of head_dim d0 + s.
   const int tr_G = lane >> 4, tr_s = lane & 15;
   const int tr_g = tr_G >> 1, tr_dh = tr_G & 1;
+  constexpr int NPV = DB * NB * 2;
+  constexpr int VPF = 2;
   auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int db = 0; db < DB; ++db) {
+    auto vread = [&](int m) __attribute__((always_inline)) {
+      const int db = m / (NB * 2), nb = (m / 2) % NB, kk = m % 2;
       const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);  // logical unit of d0 + 4*(s&3)
       const int half = (tr_s & 1) * 4;                        // element offset in the unit
+      const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
+      const int row1 = row0 + 8;
+      const s16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4_t*)(vt + row0 * D + ((u ^ swz_v<D>(row0)) * 8) + half));
+      const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (lds_s16x4_t*)(vt + row1 * D + ((u ^ swz_v<D>(row1)) * 8) + half));
+      const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
+      return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
+    };
+    u32x4_t vf[NPV];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+    for (int m = 0; m < VPF; ++m) vf[m] = vread(m);
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
-          const int row1 = row0 + 8;
-          const s16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4_t*)(vt + row0 * D + ((u ^ swz_v<D>(row0)) * 8) + half));
-          const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_s16x4_t*)(vt + row1 * D + ((u ^ swz_v<D>(row1)) * 8) + half));
-          const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
-          const u32x4_t a = {l2[0], l2[1], h2[0], h2[1]};
-          acc[db] = E::mfma(a, pb[nb][kk], acc[db]);
-        }
+    for (int m = 0; m < NPV; ++m) {
+      if (m + VPF < NPV) vf[m + VPF] = vread(m + VPF);
+      acc[m / (NB * 2)] = E::mfma(vf[m], pb[(m / 2) % NB][m % 2], acc[m / (NB * 2)]);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPF, 0);
+#pragma unroll
+    for (int m = 0; m < NPV; ++m) {
+      if (m + VPF < NPV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
   };
 
@@ -395,65 +418,50 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
 
   // ---- main loop -----------------------------------------------------------
-  // One iteration for tile t (buffer slot `slot` of t): S[t] is in `sc`
-  // (valid if live_c); S[t+1] is computed into `sn`.
-  auto step = [&](auto pred_c, auto slot, int t, f32x16_t(&sc)[NB], f32x16_t(&sn)[NB], bool live_c)
-                  __attribute__((always_inline)) -> bool {
+  // Tile t sits in buffer slot (t - t_lo) & 1 of K and V.  Step t: wait for
+  // K[t], V[t]; barrier (every wavefront done with tile t-1, whose buffers
+  // now take the loads of K[t+1], V[t+1]); S = K[t] Q^T; softmax; O += V[t]^T P.
+  auto step = [&](auto pred_c, auto slot, int t) __attribute__((always_inline)) {
     auto other = [&]() {
       if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
       else return std::integral_constant<int, 1 - decltype(slot)::value>{};
     }();
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t+1], V[t] landed
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
     __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
-    if (t + 2 < t_hi) load_tile(kbase, p.k_ss, ld_kunit, kbuf(slot), t + 2);
-    if (t + 1 < t_hi) load_tile(vbase, p.v_ss, ld_vunit, vbuf(other), t + 1);
-    const bool live_n = t + 1 < t_hi && tile_live(t + 1);
-    if (live_n) qk(kbuf(other), sn);
-    if (live_c) {
+    if (t + 1 < t_hi) {
+      load_tile(kbase, p.k_ss, ld_kunit, kbuf(other), t + 1);
+      load_tile(vbase, p.v_ss, ld_vunit, vbuf(other), t + 1);
+    }
+    if (tile_live(t)) {
       const int n0 = t * BN;
       int mcode = 1;
       if constexpr (MASK) mcode = mask_code(n0);
       if (mcode >= 0) {
+        f32x16_t sc[NB];
+        qk(kbuf(slot), sc);
         u32x4_t pb[NB][2];
         softmax(pred_c, sc, n0, mcode, pb);
         pv(vbuf(slot), pb);
       }
     }
-    return live_n;
   };
-  f32x16_t sa[NB], sb[NB];
-  bool live_a = false;
   if (t_lo < t_hi) {
     load_tile(kbase, p.k_ss, ld_kunit, kbuf(std::integral_constant<int, 0>{}), t_lo);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    live_a = tile_live(t_lo);
-    if (live_a) qk(kbuf(std::integral_constant<int, 0>{}), sa);
-    if (t_lo + 1 < t_hi) load_tile(kbase, p.k_ss, ld_kunit, kbuf(std::integral_constant<int, 1>{}), t_lo + 1);
     load_tile(vbase, p.v_ss, ld_vunit, vbuf(std::integral_constant<int, 0>{}), t_lo);
   }
-  // Full tiles run in pairs starting at an even offset from t_lo, so the
-  // buffer slots are static and S[t] / S[t+1] alternate between sa and sb
-  // without register copies (the full range is trimmed to start at an even
+  // Full tiles run in pairs starting at an even offset from t_lo, so their
+  // buffer slots are static (the full range is trimmed to start at an even
   // offset and to an even length; trimmed tiles run as edge tiles, which are
-  // always exact).  Edge tiles run one at a time and copy S[t+1] into sa.
-  auto edge_range = [&](int& t, int end) __attribute__((always_inline)) {
-    for (; t < end; ++t) {
-      const bool live_b = step(std::true_type{}, (t - t_lo) & 1, t, sa, sb, live_a);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) sa[nb] = sb[nb];
-      live_a = live_b;
-    }
-  };
+  // always exact).
   if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
   t_fhi -= (t_fhi - t_flo) & 1;
   int t = t_lo;
-  edge_range(t, t_flo);
+  for (; t < t_flo; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
   for (; t < t_fhi; t += 2) {
-    const bool live_b = step(std::false_type{}, std::integral_constant<int, 0>{}, t, sa, sb, live_a);
-    live_a = step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1, sb, sa, live_b);
+    step(std::false_type{}, std::integral_constant<int, 0>{}, t);
+    step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1);
   }
-  edge_range(t, t_hi);
+  for (; t < t_hi; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
 
   // Epilogue: O = acc / l (NaN for rows with no allowed key, like the eager
   // softmax over an all -inf row), optional log-sum-exp.
