@@ -277,13 +277,13 @@ int check_tensor(const void* ptr, const int64_t st[4], int esize) {
 // only; a configuration that is not built is rejected with
 // TRINIX_ERR_BAD_ARGUMENT).
 Cfg16 pick_cfg16(int64_t batch, int64_t hq, int64_t sq) {
-  Cfg16 c{4, 2, 64};
+  Cfg16 c{4, 2, 64, 1};
   (void)batch;
   (void)hq;
   (void)sq;
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
-    int nw = 0, occ = 0, bn = 0;
-    if (sscanf(env, "%d,%d,%d", &nw, &occ, &bn) == 3) c = Cfg16{nw, occ, bn};
+    int nw = 0, occ = 0, bn = 0, pipe = 1;
+    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &pipe) >= 3) c = Cfg16{nw, occ, bn, pipe};
   }
   return c;
 }
@@ -417,6 +417,11 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.rope_cos = (const uint16_t*)a->rope_cos;
   p.rope_sin = (const uint16_t*)a->rope_sin;
   p.rope_stride = a->rope_stride;
+  {
+    // in-tile byte offsets of up to 128 key rows stay below 2^31
+    const int64_t lim = (1ll << 31) / (2 * 128) - 128;
+    p.kv_off32 = (p.k_ss >= 0 && p.k_ss < lim && p.v_ss >= 0 && p.v_ss < lim) ? 1 : 0;
+  }
 
   hipStream_t st = (hipStream_t)stream;
   (void)hipGetLastError();

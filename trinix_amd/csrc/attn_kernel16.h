@@ -58,7 +58,23 @@ __device__ inline int swz_v(int row) {
   return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
 }
 
-template <class E, int D, int BN, int NW, int OCC, bool ALIBI, bool MASK, bool DROP>
+// Asynchronous global -> LDS copy (global_load_lds_dwordx4): lane l's 16
+// bytes at src land at LDS byte address lds_base + 16*l (lds_base wave-
+// uniform).  Issued through asm so that the compiler's wait-count analysis
+// does not see it: an LDS-writing global load makes that analysis wait for
+// all LDS reads in flight (lgkmcnt(0)) at every LDS operand use.  Callers
+// wait for these loads themselves (s_waitcnt vmcnt + barrier) before any
+// wavefront reads the LDS they fill.
+__device__ inline void dma_16b(const void* src, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_base) : "memory", "m0");
+}
+// Same, addressed as a wave-uniform 64-bit base (SGPR pair) plus a per-lane
+// 32-bit byte offset.
+__device__ inline void dma_16b_s(uint32_t offset, uint64_t base, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(offset), "s"(base), "s"(lds_base) : "memory", "m0");
+}
+
+template <class E, int D, int BN, int NW, int OCC, bool PIPE, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
   constexpr int BM = NW * 32;  // query rows per workgroup
   constexpr int DS = D / 16;   // MFMA k-steps over head_dim (QK^T)
@@ -77,6 +93,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[BN * D];
   __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[BN * D];
   __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[BN * D];
+  // third slots of the software-pipelined loop's rings (unused otherwise)
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k2[PIPE ? BN * D : 1];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v2[PIPE ? BN * D : 1];
   // Tile t lives in buffer slot (t - t_lo) & 1 of K and of V.  `slot` is a
   // std::integral_constant in the full-tile loop (static buffer choice) and
   // an int in the edge loops.
@@ -206,17 +225,48 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     ld_kunit[l] = (u % UPR) ^ swz_k<D>(ld_key[l]);
     ld_vunit[l] = (u % UPR) ^ swz_v<D>(ld_key[l]);
   }
-  // Rows past Sk are loaded from row Sk-1 (finite data): their scores are
-  // masked to -inf and their P is 0, so they never contribute.
-  auto load_tile = [&](const uint16_t* base, int64_t ss, const int* units, uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
-    const int n0 = tile * BN;
+  // Tiles inside [0, Sk) with 32-bit in-tile offsets (p.kv_off32) take the
+  // scalar-base form: the wave-uniform tile address is computed in SGPRs and
+  // each lane adds its fixed byte offset, so issuing a tile costs no vector
+  // arithmetic.  Other tiles (the last one when Sk % BN != 0) load rows past
+  // Sk from row Sk-1 (finite data): their scores are masked to -inf and
+  // their P is 0, so they never contribute.
+  uint32_t ld_koff[LPW], ld_voff[LPW];
 #pragma unroll
-    for (int l = 0; l < LPW; ++l) {
-      const int j = min(n0 + ld_key[l], p.Sk - 1);
-      const uint16_t* src = base + (int64_t)j * ss + units[l] * 8;
-      lds_void_t* dst = (lds_void_t*)((char*)lds_tile + (wave * LPW + l) * 1024);
-      __builtin_amdgcn_global_load_lds((const void*)src, dst, 16, 0, 0);
+  for (int l = 0; l < LPW; ++l) {
+    ld_koff[l] = (uint32_t)ld_key[l] * (uint32_t)p.k_ss * 2u + (uint32_t)ld_kunit[l] * 16u;
+    ld_voff[l] = (uint32_t)ld_key[l] * (uint32_t)p.v_ss * 2u + (uint32_t)ld_vunit[l] * 16u;
+  }
+  auto uniform_u64 = [](const void* ptr) __attribute__((always_inline)) -> uint64_t {
+    const uint64_t x = (uint64_t)(uintptr_t)ptr;
+    // readfirstlane returns int: widen through uint32_t (no sign extension)
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
+    return (uint64_t)lo | ((uint64_t)hi << 32);
+  };
+  const uint64_t kbase_s = uniform_u64(kbase), vbase_s = uniform_u64(vbase);
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
+  auto load_tile = [&](const uint16_t* base, uint64_t base_s, int64_t ss, const int* units, const uint32_t* offs,
+                       uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
+    const int n0 = tile * BN;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds_tile + wave_lds;
+    if (p.kv_off32 && n0 + BN <= p.Sk) {
+      const uint64_t gb = base_s + (uint64_t)n0 * (uint64_t)(ss * 2);
+#pragma unroll
+      for (int l = 0; l < LPW; ++l) dma_16b_s(offs[l], gb, lds0 + l * 1024);
+    } else {
+#pragma unroll
+      for (int l = 0; l < LPW; ++l) {
+        const int j = min(n0 + ld_key[l], p.Sk - 1);
+        dma_16b(base + (int64_t)j * ss + units[l] * 8, lds0 + l * 1024);
+      }
     }
+  };
+  auto load_k = [&](uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
+    load_tile(kbase, kbase_s, p.k_ss, ld_kunit, ld_koff, lds_tile, tile);
+  };
+  auto load_v = [&](uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
+    load_tile(vbase, vbase_s, p.v_ss, ld_vunit, ld_voff, lds_tile, tile);
   };
 
   // ---- per-tile pieces ---------------------------------------------------
@@ -238,7 +288,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // K fragments are read KPF MFMAs ahead; the sched_group_barriers keep the
   // reads ahead of their MFMAs instead of letting each MFMA wait on its read.
   constexpr int NQK = NB * DS;
-  constexpr int KPF = 3;
+  constexpr int KPF = MASK ? 3 : 6;  // mask kernels hold more live values: shorter read-ahead
   auto qk = [&](const uint16_t* kt, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
     auto kread = [&](int k) __attribute__((always_inline)) {
       const int nb = k / DS, ds = k % DS;
@@ -272,36 +322,49 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // keys kb + 4g + 0..3 of head_dim d0 + s.
   const int tr_G = lane >> 4, tr_s = lane & 15;
   const int tr_g = tr_G >> 1, tr_dh = tr_G & 1;
+  // Byte offset of this lane's first transpose read in a V tile, per 32-wide
+  // head_dim block; the other reads add constants (key rows nb*32 + kk*16
+  // and +8 keep the row swizzle).  The empty asm keeps each offset one opaque
+  // value, so every read's address is (LDS buffer + offset + constant): the
+  // compiler then attributes the read to its buffer and does not wait for
+  // global->LDS loads in flight into the other buffer.
+  int tr_off[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    const int row0 = tr_g * 4 + (tr_s >> 2);
+    const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);
+    tr_off[db] = (row0 * D + (u ^ swz_v<D>(row0)) * 8 + (tr_s & 1) * 4) * 2;
+    asm volatile("" : "+v"(tr_off[db]));
+  }
+  auto vread = [&](const uint16_t* vt, int m) __attribute__((always_inline)) {
+    const int db = m / (NB * 2), nb = (m / 2) % NB, kk = m % 2;
+    const char* base = (const char*)vt + tr_off[db] + (nb * 32 + kk * 16) * D * 2;
+    const s16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)base);
+    const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(base + 8 * D * 2));
+    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
+    return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
+  };
   constexpr int NPV = DB * NB * 2;
-  constexpr int VPF = 2;
-  auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2]) __attribute__((always_inline)) {
-    auto vread = [&](int m) __attribute__((always_inline)) {
-      const int db = m / (NB * 2), nb = (m / 2) % NB, kk = m % 2;
-      const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);  // logical unit of d0 + 4*(s&3)
-      const int half = (tr_s & 1) * 4;                        // element offset in the unit
-      const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
-      const int row1 = row0 + 8;
-      const s16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4_t*)(vt + row0 * D + ((u ^ swz_v<D>(row0)) * 8) + half));
-      const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (lds_s16x4_t*)(vt + row1 * D + ((u ^ swz_v<D>(row1)) * 8) + half));
-      const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
-      return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
-    };
+  constexpr int VPF = MASK ? 2 : 4;
+  // vpre: the first VPF fragments, read ahead (before the softmax) by the caller.
+  auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2], const u32x4_t(&vpre)[VPF]) __attribute__((always_inline)) {
     u32x4_t vf[NPV];
 #pragma unroll
-    for (int m = 0; m < VPF; ++m) vf[m] = vread(m);
+    for (int m = 0; m < VPF; ++m) vf[m] = vpre[m];
 #pragma unroll
     for (int m = 0; m < NPV; ++m) {
-      if (m + VPF < NPV) vf[m + VPF] = vread(m + VPF);
+      if (m + VPF < NPV) vf[m + VPF] = vread(vt, m + VPF);
       acc[m / (NB * 2)] = E::mfma(vf[m], pb[(m / 2) % NB][m % 2], acc[m / (NB * 2)]);
     }
-    __builtin_amdgcn_sched_group_barrier(0x100, 2 * VPF, 0);
 #pragma unroll
     for (int m = 0; m < NPV; ++m) {
       if (m + VPF < NPV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
+  };
+  auto vprefetch = [&](const uint16_t* vt, u32x4_t(&vpre)[VPF]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < VPF; ++m) vpre[m] = vread(vt, m);
   };
 
   // Softmax update of one tile; writes P^T packed as the PV B operand.
@@ -417,51 +480,247 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     return true;
   };
 
-  // ---- main loop -----------------------------------------------------------
-  // Tile t sits in buffer slot (t - t_lo) & 1 of K and V.  Step t: wait for
-  // K[t], V[t]; barrier (every wavefront done with tile t-1, whose buffers
-  // now take the loads of K[t+1], V[t+1]); S = K[t] Q^T; softmax; O += V[t]^T P.
-  auto step = [&](auto pred_c, auto slot, int t) __attribute__((always_inline)) {
-    auto other = [&]() {
-      if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
-      else return std::integral_constant<int, 1 - decltype(slot)::value>{};
-    }();
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
-    __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
-    if (t + 1 < t_hi) {
-      load_tile(kbase, p.k_ss, ld_kunit, kbuf(other), t + 1);
-      load_tile(vbase, p.v_ss, ld_vunit, vbuf(other), t + 1);
-    }
-    if (tile_live(t)) {
-      const int n0 = t * BN;
-      int mcode = 1;
-      if constexpr (MASK) mcode = mask_code(n0);
-      if (mcode >= 0) {
-        f32x16_t sc[NB];
-        qk(kbuf(slot), sc);
-        u32x4_t pb[NB][2];
-        softmax(pred_c, sc, n0, mcode, pb);
-        pv(vbuf(slot), pb);
+  if constexpr (PIPE) {
+    // ---- software-pipelined main loop (no ALiBi / mask / dropout) --------
+    // Iteration t runs the softmax of S(t) interleaved, in one straight-line
+    // block, with the MFMAs of S(t+1) = K[t+1] Q^T and of O += V[t-1]^T P(t-1),
+    // so the wavefront's own VALU work fills the MFMA pipe.  The row max and
+    // the lazy-rescale decision of tile t come first (phase 1); O is scaled
+    // after the block, once P(t-1) V(t-1) has been added under the old max.
+    // P(t_lo - 1) is zero and its V stand-in holds zeros, so the first
+    // iteration's PV adds nothing; the last iteration's QK reads a K tile
+    // past the range and its result is never used.
+    auto phase1 = [&](auto pred_c, f32x16_t(&s)[NB], int n0, float& alpha) __attribute__((always_inline)) -> bool {
+      constexpr bool PRED = decltype(pred_c)::value;
+      float mx = -INFINITY;
+      if constexpr (PRED) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int j = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+            const float x = (uint32_t)(j - jlo) <= jspan ? s[nb][v] * c : -INFINITY;
+            s[nb][v] = x;
+            mx = fmaxf(mx, x);
+          }
+        mx = xlane_max(mx);
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[nb][v]);
+        mx = xlane_max(mx) * c;
+      }
+      const bool resc = wave_any(mx > m_run + TAU);
+      if (__builtin_expect(resc, 0)) {
+        const float m_new = fmaxf(m_run, mx);
+        alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+        m_run = m_new;
+      }
+      return resc;
+    };
+    auto kread = [&](const uint16_t* kt, int k) __attribute__((always_inline)) {
+      const int nb = k / DS, ds = k % DS;
+      const int row = nb * 32 + r;
+      const int unit = (ds * 2 + g) ^ swz_k<D>(row);
+      return *(const u32x4_t*)(kt + row * D + unit * 8);
+    };
+    auto phase2 = [&](auto pred_c, const uint16_t* kt, const uint16_t* vt, f32x16_t(&s)[NB], f32x16_t(&sn)[NB],
+                      const u32x4_t(&pbp)[NB][2], u32x4_t(&pbc)[NB][2]) __attribute__((always_inline)) {
+      constexpr bool PRED = decltype(pred_c)::value;
+      // softmax element work of tile t: p = 2^(x - m), packed P^T, row sum
+      if constexpr (PRED) {
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(s[nb][v] - m_use);
+      } else {
+        const float mneg = -m_run;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][v], c, mneg));
+      }
+      float r4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          pbc[nb][kk] = (u32x4_t){E::pack(s[nb][kk * 8 + 0], s[nb][kk * 8 + 1]), E::pack(s[nb][kk * 8 + 2], s[nb][kk * 8 + 3]),
+                                  E::pack(s[nb][kk * 8 + 4], s[nb][kk * 8 + 5]), E::pack(s[nb][kk * 8 + 6], s[nb][kk * 8 + 7])};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) r4[e] = E::dot2_ones(pbc[nb][kk][e], r4[e]);
+        }
+      l_run += (r4[0] + r4[1]) + (r4[2] + r4[3]);
+      // MFMAs of S(t+1) and of O += V[t-1]^T P(t-1), alternating
+      u32x4_t kf[NQK], vf[NPV];
+#pragma unroll
+      for (int k = 0; k < KPF; ++k) kf[k] = kread(kt, k);
+#pragma unroll
+      for (int m = 0; m < VPF; ++m) vf[m] = vread(vt, m);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) sn[nb] = (f32x16_t){};
+#pragma unroll
+      for (int x = 0; x < NQK; ++x) {
+        if (x + KPF < NQK) kf[x + KPF] = kread(kt, x + KPF);
+        sn[x / DS] = E::mfma(kf[x], qr[x % DS], sn[x / DS]);
+        if (x + VPF < NPV) vf[x + VPF] = vread(vt, x + VPF);
+        acc[x / (NB * 2)] = E::mfma(vf[x], pbp[(x / 2) % NB][x % 2], acc[x / (NB * 2)]);
+      }
+      // Issue pattern per MFMA: its operand reads KPF / VPF MFMAs ahead, then
+      // about a third of the non-transcendental VALU work and one v_exp
+      // (the transcendental group mask 0x400 is separate from VALU 0x002).
+      constexpr int NEXP = NB * 16;
+      constexpr int NVALU = NB * 16 + NB * 16 + 8;  // fma/sub, pack + dot2, sums
+      constexpr int VPS = (NVALU + 2 * NQK - 1) / (2 * NQK);
+      constexpr int EPS = (NEXP + 2 * NQK - 1) / (2 * NQK);
+      __builtin_amdgcn_sched_group_barrier(0x100, KPF + 2 * VPF, 0);
+#pragma unroll
+      for (int x = 0; x < NQK; ++x) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (x + KPF < NQK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, EPS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (x + VPF < NPV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
+        __builtin_amdgcn_sched_group_barrier(0x400, EPS, 0);
+      }
+    };
+    // Three-slot rings: K[t] and V[t] live in slot (t - t_lo) % 3.  Iteration
+    // u = t - t_lo reads K[t+1] (slot (u+1)%3) and V[t-1] (slot (u+2)%3) and
+    // loads K[t+3] (slot u%3, free since K[t] was read in iteration u-1) and
+    // V[t+1] (slot (u+1)%3, free since V[t-2] was read in iteration u-1),
+    // two iterations before their use.  Every iteration issues the same
+    // 2*LPW loads (tiles past t_hi load clamped rows, never read), so the wait
+    // at its top is vmcnt(2*LPW): everything but the previous iteration's
+    // loads.  V slot 2 starts as zeros, the stand-in for V[t_lo - 1].
+    auto kslot = [&](auto c) __attribute__((always_inline)) -> uint16_t* {
+      constexpr int i = decltype(c)::value % 3;
+      return i == 0 ? lds_k0 : (i == 1 ? lds_k1 : lds_k2);
+    };
+    auto vslot = [&](auto c) __attribute__((always_inline)) -> uint16_t* {
+      constexpr int i = decltype(c)::value % 3;
+      return i == 0 ? lds_v0 : (i == 1 ? lds_v1 : lds_v2);
+    };
+    constexpr int VM_ITER = (2 * LPW & 15) | ((2 * LPW >> 4) << 14) | (7 << 4) | (15 << 8);  // vmcnt(2*LPW)
+    constexpr int VM_PRO = (3 * LPW & 15) | ((3 * LPW >> 4) << 14) | (7 << 4) | (15 << 8);   // vmcnt(3*LPW)
+    const int nt = t_hi - t_lo;
+    if (nt > 0) {
+#pragma unroll
+      for (int u = tid; u < BN * D / 8; u += NW * 64) ((u32x4_t*)lds_v2)[u] = (u32x4_t){0u, 0u, 0u, 0u};
+      load_k(lds_k0, t_lo);
+      load_k(lds_k1, t_lo + 1);
+      load_v(lds_v0, t_lo);
+      load_k(lds_k2, t_lo + 2);
+      __builtin_amdgcn_s_waitcnt(VM_PRO);  // K[t_lo]
+      __syncthreads();
+      f32x16_t sA[NB], sB[NB], sC[NB];
+      u32x4_t pA[NB][2], pB[NB][2], pC[NB][2];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) pC[nb][0] = pC[nb][1] = (u32x4_t){0u, 0u, 0u, 0u};
+      qk(lds_k0, sA);
+      auto iter = [&](auto u_c, int t, f32x16_t(&s)[NB], f32x16_t(&sn)[NB], const u32x4_t(&pbp)[NB][2],
+                      u32x4_t(&pbc)[NB][2]) __attribute__((always_inline)) {
+        constexpr int U = decltype(u_c)::value;
+        __builtin_amdgcn_s_waitcnt(VM_ITER);  // this wavefront's loads of K[t+1], V[t-1] landed
+        __syncthreads();                      // ... and every wavefront's; K[t], V[t-2] are free
+        load_k(kslot(std::integral_constant<int, U>{}), t + 3);
+        load_v(vslot(std::integral_constant<int, U + 1>{}), t + 1);
+        const uint16_t* kt = kslot(std::integral_constant<int, U + 1>{});
+        const uint16_t* vt = vslot(std::integral_constant<int, U + 2>{});
+        const int n0 = t * BN;
+        float alpha = 1.f;
+        bool resc;
+        if (t < t_flo || t >= t_fhi) {
+          resc = phase1(std::true_type{}, s, n0, alpha);
+          phase2(std::true_type{}, kt, vt, s, sn, pbp, pbc);
+        } else {
+          resc = phase1(std::false_type{}, s, n0, alpha);
+          phase2(std::false_type{}, kt, vt, s, sn, pbp, pbc);
+        }
+        if (__builtin_expect(resc, 0)) {
+#pragma unroll
+          for (int db = 0; db < DB; ++db) acc[db] *= alpha;
+        }
+      };
+      for (int t = t_lo; t < t_hi; t += 3) {
+        iter(std::integral_constant<int, 0>{}, t, sA, sB, pC, pA);
+        if (t + 1 < t_hi) iter(std::integral_constant<int, 1>{}, t + 1, sB, sC, pA, pB);
+        if (t + 2 < t_hi) iter(std::integral_constant<int, 2>{}, t + 2, sC, sA, pB, pC);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // V[t_hi - 1]
+      __syncthreads();
+      const int ul = (nt - 1) % 3;
+      u32x4_t vpre[VPF];
+      if (ul == 0) {
+        vprefetch(lds_v0, vpre);
+        pv(lds_v0, pA, vpre);
+      } else if (ul == 1) {
+        vprefetch(lds_v1, vpre);
+        pv(lds_v1, pB, vpre);
+      } else {
+        vprefetch(lds_v2, vpre);
+        pv(lds_v2, pC, vpre);
       }
     }
-  };
-  if (t_lo < t_hi) {
-    load_tile(kbase, p.k_ss, ld_kunit, kbuf(std::integral_constant<int, 0>{}), t_lo);
-    load_tile(vbase, p.v_ss, ld_vunit, vbuf(std::integral_constant<int, 0>{}), t_lo);
+  } else {
+    // ---- main loop -----------------------------------------------------------
+    // Tile t sits in buffer slot (t - t_lo) & 1 of K and V.  Step t: wait for
+    // K[t], V[t]; barrier (every wavefront done with tile t-1, whose buffers
+    // now take the loads of K[t+1], V[t+1]); S = K[t] Q^T; softmax; O += V[t]^T P.
+    auto step = [&](auto pred_c, auto slot, int t) __attribute__((always_inline)) {
+      auto other = [&]() {
+        if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
+        else return std::integral_constant<int, 1 - decltype(slot)::value>{};
+      }();
+      __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
+      __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
+      if (t + 1 < t_hi) {
+        load_k(kbuf(other), t + 1);
+        load_v(vbuf(other), t + 1);
+      }
+      if (tile_live(t)) {
+        const int n0 = t * BN;
+        int mcode = 1;
+        if constexpr (MASK) mcode = mask_code(n0);
+        if (mcode >= 0) {
+          // MFMA sections at raised priority: the other wavefront on this SIMD
+          // fills the MFMA pipe gaps with its softmax VALU work.
+          f32x16_t sc[NB];
+          u32x4_t vpre[VPF];
+          __builtin_amdgcn_s_setprio(1);
+          qk(kbuf(slot), sc);
+          vprefetch(vbuf(slot), vpre);  // V operand reads in flight during the softmax
+          __builtin_amdgcn_s_setprio(0);
+          u32x4_t pb[NB][2];
+          softmax(pred_c, sc, n0, mcode, pb);
+          __builtin_amdgcn_s_setprio(1);
+          pv(vbuf(slot), pb, vpre);
+          __builtin_amdgcn_s_setprio(0);
+        }
+      }
+    };
+    if (t_lo < t_hi) {
+      load_k(kbuf(std::integral_constant<int, 0>{}), t_lo);
+      load_v(vbuf(std::integral_constant<int, 0>{}), t_lo);
+    }
+    // Full tiles run in pairs starting at an even offset from t_lo, so their
+    // buffer slots are static (the full range is trimmed to start at an even
+    // offset and to an even length; trimmed tiles run as edge tiles, which are
+    // always exact).
+    if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
+    t_fhi -= (t_fhi - t_flo) & 1;
+    int t = t_lo;
+    for (; t < t_flo; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
+    for (; t < t_fhi; t += 2) {
+      step(std::false_type{}, std::integral_constant<int, 0>{}, t);
+      step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1);
+    }
+    for (; t < t_hi; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
   }
-  // Full tiles run in pairs starting at an even offset from t_lo, so their
-  // buffer slots are static (the full range is trimmed to start at an even
-  // offset and to an even length; trimmed tiles run as edge tiles, which are
-  // always exact).
-  if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
-  t_fhi -= (t_fhi - t_flo) & 1;
-  int t = t_lo;
-  for (; t < t_flo; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
-  for (; t < t_fhi; t += 2) {
-    step(std::false_type{}, std::integral_constant<int, 0>{}, t);
-    step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1);
-  }
-  for (; t < t_hi; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
 
   // Epilogue: O = acc / l (NaN for rows with no allowed key, like the eager
   // softmax over an all -inf row), optional log-sum-exp.
@@ -482,14 +741,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   }
 }
 
-// Launcher of one (dtype, D, tile shape): every feature combination.
+// Launcher of the (nw, occ) = (4, 2) tile shape: every feature combination.
 template <class E, int D, int BN, int NW, int OCC>
 hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   const dim3 grid((unsigned)p.total_work), block(NW * 64);
   switch (feat) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,         \
+    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, false, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,  \
                                         (F & kFeatDropout) != 0>),                                              \
                        grid, block, 0, st, p);                                                                  \
     return hipGetLastError();
@@ -506,20 +765,25 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   }
 }
 
-// One tile shape without ALiBi / mask / dropout (tuning sweeps).
-template <class E, int D, int BN, int NW, int OCC>
-hipError_t launch_plain(const FwdParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, false, false, false>), dim3((unsigned)p.total_work),
-                     dim3(NW * 64), 0, st, p);
+// One wavefront per SIMD (occ 1), no features: the software-pipelined loop
+// (pipe) or the plain one.
+template <class E, int D, int BN, int NW>
+hipError_t launch_occ1(const FwdParams& p, bool pipe, hipStream_t st) {
+  const dim3 grid((unsigned)p.total_work), block(NW * 64);
+  if (pipe)
+    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, 1, true, false, false, false>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, 1, false, false, false, false>), grid, block, 0, st, p);
   return hipGetLastError();
 }
 
 // Tile configs built for every (dtype, D): (nw, occ, bn) = (4, 2, 64) with
-// every feature combination and (4, 1, 64) without features.
+// every feature combination, (4, 1, 64) without features.
 #define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                              \
   hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                           \
     if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 2) return launch_feat<E, D, 64, 4, 2>(p, feat, st);  \
-    if (feat == 0 && cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 1) return launch_plain<E, D, 64, 4, 1>(p, st); \
+    if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 1 && feat == 0)                                       \
+      return launch_occ1<E, D, 64, 4>(p, cfg.pipe != 0, st);                                           \
     return hipErrorInvalidValue;                                                                        \
   }
 
