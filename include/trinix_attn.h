@@ -46,7 +46,7 @@ typedef enum trinix_status {
   TRINIX_ERR_BAD_DTYPE = 2,      /* unsupported dtype / dtype mismatch      */
   TRINIX_ERR_BAD_HEAD_DIM = 3,   /* head_dim not in {64, 128}               */
   TRINIX_ERR_BAD_SHAPE = 4,      /* non-positive or inconsistent sizes      */
-  TRINIX_ERR_BAD_STRIDE = 5,     /* d-stride != 1 or misaligned rows        */
+  TRINIX_ERR_BAD_STRIDE = 5,     /* d-stride != 1, misaligned rows, or a 16-bit K/V key-row stride >= 2^22 elements */
   TRINIX_ERR_BAD_ARGUMENT = 6,   /* other invalid argument (dropout, ...)   */
   TRINIX_ERR_NO_DEVICE = 7,      /* no gfx950 device / HIP runtime error    */
   TRINIX_ERR_LAUNCH = 8          /* hipGetLastError after the launch        */

@@ -258,6 +258,8 @@ constexpr int kWavesF32 = 4;
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
+constexpr int64_t kMaxKvRowStride = 1ll << 22;  // elements; 128 rows * 2 B * 2^22 = 2^30 bytes
+
 int check_tensor(const void* ptr, const int64_t st[4], int esize) {
   if (!ptr) return TRINIX_ERR_NULL_POINTER;
   if (st[3] != 1) return TRINIX_ERR_BAD_STRIDE;
@@ -277,13 +279,13 @@ int check_tensor(const void* ptr, const int64_t st[4], int esize) {
 // only; a configuration that is not built is rejected with
 // TRINIX_ERR_BAD_ARGUMENT).
 Cfg16 pick_cfg16(int64_t batch, int64_t hq, int64_t sq) {
-  Cfg16 c{4, 2, 64, 1};
+  Cfg16 c{4, 2, 64};
   (void)batch;
   (void)hq;
   (void)sq;
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
-    int nw = 0, occ = 0, bn = 0, pipe = 1;
-    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &pipe) >= 3) c = Cfg16{nw, occ, bn, pipe};
+    int nw = 0, occ = 0, bn = 0;
+    if (sscanf(env, "%d,%d,%d", &nw, &occ, &bn) == 3) c = Cfg16{nw, occ, bn};
   }
   return c;
 }
@@ -301,7 +303,7 @@ const char* trinix_status_string(int status) {
     case TRINIX_ERR_BAD_DTYPE: return "unsupported dtype";
     case TRINIX_ERR_BAD_HEAD_DIM: return "unsupported head_dim (kernels are built for 64 and 128)";
     case TRINIX_ERR_BAD_SHAPE: return "invalid or inconsistent sizes";
-    case TRINIX_ERR_BAD_STRIDE: return "unsupported strides or alignment (head_dim stride must be 1, 16-byte aligned rows)";
+    case TRINIX_ERR_BAD_STRIDE: return "unsupported strides or alignment (head_dim stride must be 1, 16-byte aligned rows, 16-bit K/V key-row stride below 2^22 elements)";
     case TRINIX_ERR_BAD_ARGUMENT: return "invalid argument";
     case TRINIX_ERR_NO_DEVICE: return "no gfx950 device available";
     case TRINIX_ERR_LAUNCH: return "kernel launch failed";
@@ -355,6 +357,11 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   if ((rc = check_tensor(a->q, a->q_stride, esize))) return rc;
   if ((rc = check_tensor(a->k, a->k_stride, esize))) return rc;
   if ((rc = check_tensor(a->v, a->v_stride, esize))) return rc;
+  // 16-bit kernels address a K/V tile (up to 128 key rows) as one base plus
+  // per-lane 32-bit byte offsets: the key-row stride must be in [0, 2^22).
+  if (esize == 2 && (a->k_stride[1] < 0 || a->k_stride[1] >= kMaxKvRowStride || a->v_stride[1] < 0 ||
+                     a->v_stride[1] >= kMaxKvRowStride))
+    return TRINIX_ERR_BAD_STRIDE;
   if ((rc = check_tensor(a->out, a->out_stride, esize))) return rc;
   if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
       a->mask_dtype != TRINIX_U8)
@@ -417,11 +424,6 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.rope_cos = (const uint16_t*)a->rope_cos;
   p.rope_sin = (const uint16_t*)a->rope_sin;
   p.rope_stride = a->rope_stride;
-  {
-    // in-tile byte offsets of up to 128 key rows stay below 2^31
-    const int64_t lim = (1ll << 31) / (2 * 128) - 128;
-    p.kv_off32 = (p.k_ss >= 0 && p.k_ss < lim && p.v_ss >= 0 && p.v_ss < lim) ? 1 : 0;
-  }
 
   hipStream_t st = (hipStream_t)stream;
   (void)hipGetLastError();

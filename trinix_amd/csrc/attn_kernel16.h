@@ -59,22 +59,18 @@ __device__ inline int swz_v(int row) {
 }
 
 // Asynchronous global -> LDS copy (global_load_lds_dwordx4): lane l's 16
-// bytes at src land at LDS byte address lds_base + 16*l (lds_base wave-
-// uniform).  Issued through asm so that the compiler's wait-count analysis
+// bytes land at LDS byte address lds_base + 16*l (lds_base wave-uniform).  Issued through asm so that the compiler's wait-count analysis
 // does not see it: an LDS-writing global load makes that analysis wait for
 // all LDS reads in flight (lgkmcnt(0)) at every LDS operand use.  Callers
 // wait for these loads themselves (s_waitcnt vmcnt + barrier) before any
 // wavefront reads the LDS they fill.
-__device__ inline void dma_16b(const void* src, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds_base) : "memory", "m0");
-}
-// Same, addressed as a wave-uniform 64-bit base (SGPR pair) plus a per-lane
-// 32-bit byte offset.
+// The global address is a wave-uniform 64-bit base (SGPR pair) plus a
+// per-lane 32-bit byte offset.
 __device__ inline void dma_16b_s(uint32_t offset, uint64_t base, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(offset), "s"(base), "s"(lds_base) : "memory", "m0");
 }
 
-template <class E, int D, int BN, int NW, int OCC, bool PIPE, bool ALIBI, bool MASK, bool DROP>
+template <class E, int D, int BN, int NW, int OCC, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
   constexpr int BM = NW * 32;  // query rows per workgroup
   constexpr int DS = D / 16;   // MFMA k-steps over head_dim (QK^T)
@@ -93,9 +89,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[BN * D];
   __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[BN * D];
   __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[BN * D];
-  // third slots of the software-pipelined loop's rings (unused otherwise)
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_k2[PIPE ? BN * D : 1];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_v2[PIPE ? BN * D : 1];
   // Tile t lives in buffer slot (t - t_lo) & 1 of K and of V.  `slot` is a
   // std::integral_constant in the full-tile loop (static buffer choice) and
   // an int in the edge loops.
@@ -108,7 +101,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     else return decltype(slot)::value ? lds_v1 : lds_v0;
   };
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane & 31, g = lane >> 5;
 
   // work item: (b, kv-head, m-block, q-head within the group), the q-heads
@@ -214,28 +208,23 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // ---- direct global -> LDS tile loads --------------------------------
   // Load l of this wavefront fills LDS units [64*(wave*LPW + l), +64) of the
   // tile (one per lane); unit u holds key row u / UPR, physical unit u % UPR,
-  // i.e. logical 16-byte unit (u % UPR) ^ swz(row) of that row.
+  // i.e. logical 16-byte unit (u % UPR) ^ swz(row) of that row.  A tile is
+  // addressed as a wave-uniform base in SGPRs (the tile's first row) plus a
+  // per-lane 32-bit byte offset (the host guarantees BN rows of K/V span
+  // less than 2^31 bytes), so issuing a tile costs no vector arithmetic.
+  // In a tile reaching past Sk (the last one when Sk % BN != 0) rows past
+  // Sk are loaded from row Sk-1 (finite data): their scores are masked to
+  // -inf and their P is 0, so they never contribute.
   const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  int ld_key[LPW], ld_kunit[LPW], ld_vunit[LPW];
-#pragma unroll
-  for (int l = 0; l < LPW; ++l) {
-    const int u = (wave * LPW + l) * 64 + lane;
-    ld_key[l] = u / UPR;
-    ld_kunit[l] = (u % UPR) ^ swz_k<D>(ld_key[l]);
-    ld_vunit[l] = (u % UPR) ^ swz_v<D>(ld_key[l]);
-  }
-  // Tiles inside [0, Sk) with 32-bit in-tile offsets (p.kv_off32) take the
-  // scalar-base form: the wave-uniform tile address is computed in SGPRs and
-  // each lane adds its fixed byte offset, so issuing a tile costs no vector
-  // arithmetic.  Other tiles (the last one when Sk % BN != 0) load rows past
-  // Sk from row Sk-1 (finite data): their scores are masked to -inf and
-  // their P is 0, so they never contribute.
+  auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
+  auto ld_unit_k = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_k<D>(ld_row(l)); };
+  auto ld_unit_v = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_v<D>(ld_row(l)); };
   uint32_t ld_koff[LPW], ld_voff[LPW];
 #pragma unroll
   for (int l = 0; l < LPW; ++l) {
-    ld_koff[l] = (uint32_t)ld_key[l] * (uint32_t)p.k_ss * 2u + (uint32_t)ld_kunit[l] * 16u;
-    ld_voff[l] = (uint32_t)ld_key[l] * (uint32_t)p.v_ss * 2u + (uint32_t)ld_vunit[l] * 16u;
+    ld_koff[l] = (uint32_t)ld_row(l) * (uint32_t)p.k_ss * 2u + (uint32_t)ld_unit_k(l) * 16u;
+    ld_voff[l] = (uint32_t)ld_row(l) * (uint32_t)p.v_ss * 2u + (uint32_t)ld_unit_v(l) * 16u;
   }
   auto uniform_u64 = [](const void* ptr) __attribute__((always_inline)) -> uint64_t {
     const uint64_t x = (uint64_t)(uintptr_t)ptr;
@@ -246,27 +235,29 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
   const uint64_t kbase_s = uniform_u64(kbase), vbase_s = uniform_u64(vbase);
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
-  auto load_tile = [&](const uint16_t* base, uint64_t base_s, int64_t ss, const int* units, const uint32_t* offs,
-                       uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
+  auto load_tile = [&](bool is_k, uint64_t base_s, int64_t ss, const uint32_t* offs, uint16_t* lds_tile, int tile)
+                       __attribute__((always_inline)) {
     const int n0 = tile * BN;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds_tile + wave_lds;
-    if (p.kv_off32 && n0 + BN <= p.Sk) {
-      const uint64_t gb = base_s + (uint64_t)n0 * (uint64_t)(ss * 2);
+    const uint64_t gb = base_s + (uint64_t)n0 * (uint64_t)(ss * 2);
+    if (n0 + BN <= p.Sk) {
 #pragma unroll
-      for (int l = 0; l < LPW; ++l) dma_16b_s(offs[l], gb, lds0 + l * 1024);
+      for (int l = 0; l < LPW; ++l) dma_16b_s(offs[l], gb, __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
     } else {
+      const int last = p.Sk - 1 - n0;  // >= 0: tiles start below Sk
 #pragma unroll
       for (int l = 0; l < LPW; ++l) {
-        const int j = min(n0 + ld_key[l], p.Sk - 1);
-        dma_16b(base + (int64_t)j * ss + units[l] * 8, lds0 + l * 1024);
+        const uint32_t row = (uint32_t)min(ld_row(l), last);
+        const uint32_t unit = (uint32_t)(is_k ? ld_unit_k(l) : ld_unit_v(l));
+        dma_16b_s(row * (uint32_t)ss * 2u + unit * 16u, gb, __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
       }
     }
   };
   auto load_k = [&](uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
-    load_tile(kbase, kbase_s, p.k_ss, ld_kunit, ld_koff, lds_tile, tile);
+    load_tile(true, kbase_s, p.k_ss, ld_koff, lds_tile, tile);
   };
   auto load_v = [&](uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
-    load_tile(vbase, vbase_s, p.v_ss, ld_vunit, ld_voff, lds_tile, tile);
+    load_tile(false, vbase_s, p.v_ss, ld_voff, lds_tile, tile);
   };
 
   // ---- per-tile pieces ---------------------------------------------------
@@ -289,12 +280,19 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // reads ahead of their MFMAs instead of letting each MFMA wait on its read.
   constexpr int NQK = NB * DS;
   constexpr int KPF = MASK ? 3 : 6;  // mask kernels hold more live values: shorter read-ahead
+  // Byte offset of K fragment (nb, ds) of this lane in a K tile: row
+  // nb*32 + r, unit (2ds + g) ^ swz_k(r) (the swizzle depends only on r).  As
+  // 16*((2ds) ^ (g ^ swz)) = 32*ds ^ 16*(g ^ swz) and the row offset has no
+  // bits below bit 8, it is nb*32*D*2 + (k_lane ^ 32*ds): one register, one
+  // v_xor per read (kept at the read by the empty asm, instead of eight
+  // loop-invariant addresses held in registers).
+  const uint32_t k_lane = (uint32_t)(r * D * 2 + 16 * (g ^ swz_k<D>(r)));
   auto qk = [&](const uint16_t* kt, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
     auto kread = [&](int k) __attribute__((always_inline)) {
       const int nb = k / DS, ds = k % DS;
-      const int row = nb * 32 + r;
-      const int unit = (ds * 2 + g) ^ swz_k<D>(row);
-      return *(const u32x4_t*)(kt + row * D + unit * 8);
+      uint32_t off = k_lane ^ (uint32_t)(ds << 5);
+      asm volatile("" : "+v"(off));
+      return *(const u32x4_t*)((const char*)kt + nb * 32 * D * 2 + off);
     };
     u32x4_t kf[NQK];
 #pragma unroll
@@ -480,247 +478,59 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     return true;
   };
 
-  if constexpr (PIPE) {
-    // ---- software-pipelined main loop (no ALiBi / mask / dropout) --------
-    // Iteration t runs the softmax of S(t) interleaved, in one straight-line
-    // block, with the MFMAs of S(t+1) = K[t+1] Q^T and of O += V[t-1]^T P(t-1),
-    // so the wavefront's own VALU work fills the MFMA pipe.  The row max and
-    // the lazy-rescale decision of tile t come first (phase 1); O is scaled
-    // after the block, once P(t-1) V(t-1) has been added under the old max.
-    // P(t_lo - 1) is zero and its V stand-in holds zeros, so the first
-    // iteration's PV adds nothing; the last iteration's QK reads a K tile
-    // past the range and its result is never used.
-    auto phase1 = [&](auto pred_c, f32x16_t(&s)[NB], int n0, float& alpha) __attribute__((always_inline)) -> bool {
-      constexpr bool PRED = decltype(pred_c)::value;
-      float mx = -INFINITY;
-      if constexpr (PRED) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int j = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-            const float x = (uint32_t)(j - jlo) <= jspan ? s[nb][v] * c : -INFINITY;
-            s[nb][v] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = xlane_max(mx);
-      } else {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[nb][v]);
-        mx = xlane_max(mx) * c;
-      }
-      const bool resc = wave_any(mx > m_run + TAU);
-      if (__builtin_expect(resc, 0)) {
-        const float m_new = fmaxf(m_run, mx);
-        alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
-        m_run = m_new;
-      }
-      return resc;
-    };
-    auto kread = [&](const uint16_t* kt, int k) __attribute__((always_inline)) {
-      const int nb = k / DS, ds = k % DS;
-      const int row = nb * 32 + r;
-      const int unit = (ds * 2 + g) ^ swz_k<D>(row);
-      return *(const u32x4_t*)(kt + row * D + unit * 8);
-    };
-    auto phase2 = [&](auto pred_c, const uint16_t* kt, const uint16_t* vt, f32x16_t(&s)[NB], f32x16_t(&sn)[NB],
-                      const u32x4_t(&pbp)[NB][2], u32x4_t(&pbc)[NB][2]) __attribute__((always_inline)) {
-      constexpr bool PRED = decltype(pred_c)::value;
-      // softmax element work of tile t: p = 2^(x - m), packed P^T, row sum
-      if constexpr (PRED) {
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(s[nb][v] - m_use);
-      } else {
-        const float mneg = -m_run;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[nb][v], c, mneg));
-      }
-      float r4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          pbc[nb][kk] = (u32x4_t){E::pack(s[nb][kk * 8 + 0], s[nb][kk * 8 + 1]), E::pack(s[nb][kk * 8 + 2], s[nb][kk * 8 + 3]),
-                                  E::pack(s[nb][kk * 8 + 4], s[nb][kk * 8 + 5]), E::pack(s[nb][kk * 8 + 6], s[nb][kk * 8 + 7])};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) r4[e] = E::dot2_ones(pbc[nb][kk][e], r4[e]);
-        }
-      l_run += (r4[0] + r4[1]) + (r4[2] + r4[3]);
-      // MFMAs of S(t+1) and of O += V[t-1]^T P(t-1), alternating
-      u32x4_t kf[NQK], vf[NPV];
-#pragma unroll
-      for (int k = 0; k < KPF; ++k) kf[k] = kread(kt, k);
-#pragma unroll
-      for (int m = 0; m < VPF; ++m) vf[m] = vread(vt, m);
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) sn[nb] = (f32x16_t){};
-#pragma unroll
-      for (int x = 0; x < NQK; ++x) {
-        if (x + KPF < NQK) kf[x + KPF] = kread(kt, x + KPF);
-        sn[x / DS] = E::mfma(kf[x], qr[x % DS], sn[x / DS]);
-        if (x + VPF < NPV) vf[x + VPF] = vread(vt, x + VPF);
-        acc[x / (NB * 2)] = E::mfma(vf[x], pbp[(x / 2) % NB][x % 2], acc[x / (NB * 2)]);
-      }
-      // Issue pattern per MFMA: its operand reads KPF / VPF MFMAs ahead, then
-      // about a third of the non-transcendental VALU work and one v_exp
-      // (the transcendental group mask 0x400 is separate from VALU 0x002).
-      constexpr int NEXP = NB * 16;
-      constexpr int NVALU = NB * 16 + NB * 16 + 8;  // fma/sub, pack + dot2, sums
-      constexpr int VPS = (NVALU + 2 * NQK - 1) / (2 * NQK);
-      constexpr int EPS = (NEXP + 2 * NQK - 1) / (2 * NQK);
-      __builtin_amdgcn_sched_group_barrier(0x100, KPF + 2 * VPF, 0);
-#pragma unroll
-      for (int x = 0; x < NQK; ++x) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (x + KPF < NQK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
-        __builtin_amdgcn_sched_group_barrier(0x400, EPS, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (x + VPF < NPV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, VPS, 0);
-        __builtin_amdgcn_sched_group_barrier(0x400, EPS, 0);
-      }
-    };
-    // Three-slot rings: K[t] and V[t] live in slot (t - t_lo) % 3.  Iteration
-    // u = t - t_lo reads K[t+1] (slot (u+1)%3) and V[t-1] (slot (u+2)%3) and
-    // loads K[t+3] (slot u%3, free since K[t] was read in iteration u-1) and
-    // V[t+1] (slot (u+1)%3, free since V[t-2] was read in iteration u-1),
-    // two iterations before their use.  Every iteration issues the same
-    // 2*LPW loads (tiles past t_hi load clamped rows, never read), so the wait
-    // at its top is vmcnt(2*LPW): everything but the previous iteration's
-    // loads.  V slot 2 starts as zeros, the stand-in for V[t_lo - 1].
-    auto kslot = [&](auto c) __attribute__((always_inline)) -> uint16_t* {
-      constexpr int i = decltype(c)::value % 3;
-      return i == 0 ? lds_k0 : (i == 1 ? lds_k1 : lds_k2);
-    };
-    auto vslot = [&](auto c) __attribute__((always_inline)) -> uint16_t* {
-      constexpr int i = decltype(c)::value % 3;
-      return i == 0 ? lds_v0 : (i == 1 ? lds_v1 : lds_v2);
-    };
-    constexpr int VM_ITER = (2 * LPW & 15) | ((2 * LPW >> 4) << 14) | (7 << 4) | (15 << 8);  // vmcnt(2*LPW)
-    constexpr int VM_PRO = (3 * LPW & 15) | ((3 * LPW >> 4) << 14) | (7 << 4) | (15 << 8);   // vmcnt(3*LPW)
-    const int nt = t_hi - t_lo;
-    if (nt > 0) {
-#pragma unroll
-      for (int u = tid; u < BN * D / 8; u += NW * 64) ((u32x4_t*)lds_v2)[u] = (u32x4_t){0u, 0u, 0u, 0u};
-      load_k(lds_k0, t_lo);
-      load_k(lds_k1, t_lo + 1);
-      load_v(lds_v0, t_lo);
-      load_k(lds_k2, t_lo + 2);
-      __builtin_amdgcn_s_waitcnt(VM_PRO);  // K[t_lo]
-      __syncthreads();
-      f32x16_t sA[NB], sB[NB], sC[NB];
-      u32x4_t pA[NB][2], pB[NB][2], pC[NB][2];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) pC[nb][0] = pC[nb][1] = (u32x4_t){0u, 0u, 0u, 0u};
-      qk(lds_k0, sA);
-      auto iter = [&](auto u_c, int t, f32x16_t(&s)[NB], f32x16_t(&sn)[NB], const u32x4_t(&pbp)[NB][2],
-                      u32x4_t(&pbc)[NB][2]) __attribute__((always_inline)) {
-        constexpr int U = decltype(u_c)::value;
-        __builtin_amdgcn_s_waitcnt(VM_ITER);  // this wavefront's loads of K[t+1], V[t-1] landed
-        __syncthreads();                      // ... and every wavefront's; K[t], V[t-2] are free
-        load_k(kslot(std::integral_constant<int, U>{}), t + 3);
-        load_v(vslot(std::integral_constant<int, U + 1>{}), t + 1);
-        const uint16_t* kt = kslot(std::integral_constant<int, U + 1>{});
-        const uint16_t* vt = vslot(std::integral_constant<int, U + 2>{});
-        const int n0 = t * BN;
-        float alpha = 1.f;
-        bool resc;
-        if (t < t_flo || t >= t_fhi) {
-          resc = phase1(std::true_type{}, s, n0, alpha);
-          phase2(std::true_type{}, kt, vt, s, sn, pbp, pbc);
-        } else {
-          resc = phase1(std::false_type{}, s, n0, alpha);
-          phase2(std::false_type{}, kt, vt, s, sn, pbp, pbc);
-        }
-        if (__builtin_expect(resc, 0)) {
-#pragma unroll
-          for (int db = 0; db < DB; ++db) acc[db] *= alpha;
-        }
-      };
-      for (int t = t_lo; t < t_hi; t += 3) {
-        iter(std::integral_constant<int, 0>{}, t, sA, sB, pC, pA);
-        if (t + 1 < t_hi) iter(std::integral_constant<int, 1>{}, t + 1, sB, sC, pA, pB);
-        if (t + 2 < t_hi) iter(std::integral_constant<int, 2>{}, t + 2, sC, sA, pB, pC);
-      }
-      __builtin_amdgcn_s_waitcnt(0);  // V[t_hi - 1]
-      __syncthreads();
-      const int ul = (nt - 1) % 3;
-      u32x4_t vpre[VPF];
-      if (ul == 0) {
-        vprefetch(lds_v0, vpre);
-        pv(lds_v0, pA, vpre);
-      } else if (ul == 1) {
-        vprefetch(lds_v1, vpre);
-        pv(lds_v1, pB, vpre);
-      } else {
-        vprefetch(lds_v2, vpre);
-        pv(lds_v2, pC, vpre);
+  // ---- main loop -----------------------------------------------------------
+  // Tile t sits in buffer slot (t - t_lo) & 1 of K and V.  Step t: wait for
+  // K[t], V[t]; barrier (every wavefront done with tile t-1, whose buffers
+  // now take the loads of K[t+1], V[t+1]); S = K[t] Q^T; softmax; O += V[t]^T P.
+  auto step = [&](auto pred_c, auto slot, int t) __attribute__((always_inline)) {
+    auto other = [&]() {
+      if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
+      else return std::integral_constant<int, 1 - decltype(slot)::value>{};
+    }();
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
+    __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
+    if (t + 1 < t_hi) {
+      load_k(kbuf(other), t + 1);
+      load_v(vbuf(other), t + 1);
+    }
+    if (tile_live(t)) {
+      const int n0 = t * BN;
+      int mcode = 1;
+      if constexpr (MASK) mcode = mask_code(n0);
+      if (mcode >= 0) {
+        // MFMA sections at raised priority: the other wavefront on this SIMD
+        // fills the MFMA pipe gaps with its softmax VALU work.
+        f32x16_t sc[NB];
+        u32x4_t vpre[VPF];
+        __builtin_amdgcn_s_setprio(1);
+        qk(kbuf(slot), sc);
+        vprefetch(vbuf(slot), vpre);  // V operand reads in flight during the softmax
+        __builtin_amdgcn_s_setprio(0);
+        u32x4_t pb[NB][2];
+        softmax(pred_c, sc, n0, mcode, pb);
+        __builtin_amdgcn_s_setprio(1);
+        pv(vbuf(slot), pb, vpre);
+        __builtin_amdgcn_s_setprio(0);
       }
     }
-  } else {
-    // ---- main loop -----------------------------------------------------------
-    // Tile t sits in buffer slot (t - t_lo) & 1 of K and V.  Step t: wait for
-    // K[t], V[t]; barrier (every wavefront done with tile t-1, whose buffers
-    // now take the loads of K[t+1], V[t+1]); S = K[t] Q^T; softmax; O += V[t]^T P.
-    auto step = [&](auto pred_c, auto slot, int t) __attribute__((always_inline)) {
-      auto other = [&]() {
-        if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
-        else return std::integral_constant<int, 1 - decltype(slot)::value>{};
-      }();
-      __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
-      __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
-      if (t + 1 < t_hi) {
-        load_k(kbuf(other), t + 1);
-        load_v(vbuf(other), t + 1);
-      }
-      if (tile_live(t)) {
-        const int n0 = t * BN;
-        int mcode = 1;
-        if constexpr (MASK) mcode = mask_code(n0);
-        if (mcode >= 0) {
-          // MFMA sections at raised priority: the other wavefront on this SIMD
-          // fills the MFMA pipe gaps with its softmax VALU work.
-          f32x16_t sc[NB];
-          u32x4_t vpre[VPF];
-          __builtin_amdgcn_s_setprio(1);
-          qk(kbuf(slot), sc);
-          vprefetch(vbuf(slot), vpre);  // V operand reads in flight during the softmax
-          __builtin_amdgcn_s_setprio(0);
-          u32x4_t pb[NB][2];
-          softmax(pred_c, sc, n0, mcode, pb);
-          __builtin_amdgcn_s_setprio(1);
-          pv(vbuf(slot), pb, vpre);
-          __builtin_amdgcn_s_setprio(0);
-        }
-      }
-    };
-    if (t_lo < t_hi) {
-      load_k(kbuf(std::integral_constant<int, 0>{}), t_lo);
-      load_v(vbuf(std::integral_constant<int, 0>{}), t_lo);
-    }
-    // Full tiles run in pairs starting at an even offset from t_lo, so their
-    // buffer slots are static (the full range is trimmed to start at an even
-    // offset and to an even length; trimmed tiles run as edge tiles, which are
-    // always exact).
-    if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
-    t_fhi -= (t_fhi - t_flo) & 1;
-    int t = t_lo;
-    for (; t < t_flo; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
-    for (; t < t_fhi; t += 2) {
-      step(std::false_type{}, std::integral_constant<int, 0>{}, t);
-      step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1);
-    }
-    for (; t < t_hi; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
+  };
+  if (t_lo < t_hi) {
+    load_k(kbuf(std::integral_constant<int, 0>{}), t_lo);
+    load_v(vbuf(std::integral_constant<int, 0>{}), t_lo);
   }
+  // Full tiles run in pairs starting at an even offset from t_lo, so their
+  // buffer slots are static (the full range is trimmed to start at an even
+  // offset and to an even length; trimmed tiles run as edge tiles, which are
+  // always exact).
+  if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
+  t_fhi -= (t_fhi - t_flo) & 1;
+  int t = t_lo;
+  for (; t < t_flo; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
+  for (; t < t_fhi; t += 2) {
+    step(std::false_type{}, std::integral_constant<int, 0>{}, t);
+    step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1);
+  }
+  for (; t < t_hi; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
 
   // Epilogue: O = acc / l (NaN for rows with no allowed key, like the eager
   // softmax over an all -inf row), optional log-sum-exp.
@@ -748,7 +558,7 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   switch (feat) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, false, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,  \
+    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,         \
                                         (F & kFeatDropout) != 0>),                                              \
                        grid, block, 0, st, p);                                                                  \
     return hipGetLastError();
@@ -765,25 +575,11 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   }
 }
 
-// One wavefront per SIMD (occ 1), no features: the software-pipelined loop
-// (pipe) or the plain one.
-template <class E, int D, int BN, int NW>
-hipError_t launch_occ1(const FwdParams& p, bool pipe, hipStream_t st) {
-  const dim3 grid((unsigned)p.total_work), block(NW * 64);
-  if (pipe)
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, 1, true, false, false, false>), grid, block, 0, st, p);
-  else
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, 1, false, false, false, false>), grid, block, 0, st, p);
-  return hipGetLastError();
-}
-
-// Tile configs built for every (dtype, D): (nw, occ, bn) = (4, 2, 64) with
-// every feature combination, (4, 1, 64) without features.
+// Tile config built for every (dtype, D): (nw, occ, bn) = (4, 2, 64), every
+// feature combination.
 #define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                              \
   hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                           \
     if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 2) return launch_feat<E, D, 64, 4, 2>(p, feat, st);  \
-    if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 1 && feat == 0)                                       \
-      return launch_occ1<E, D, 64, 4>(p, cfg.pipe != 0, st);                                           \
     return hipErrorInvalidValue;                                                                        \
   }
 

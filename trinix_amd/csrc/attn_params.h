@@ -36,7 +36,6 @@ struct FwdParams {
   const uint16_t* rope_cos;
   const uint16_t* rope_sin;
   int64_t rope_stride;
-  int kv_off32;  // K/V byte offsets within a tile of up to 128 keys fit in 31 bits
 };
 
 // Tile shape of one 16-bit kernel instantiation.
@@ -44,7 +43,6 @@ struct Cfg16 {
   int nw;   // wavefronts per workgroup (32 query rows each)
   int occ;  // target wavefronts per SIMD (register budget 512 / occ)
   int bn;   // keys per K/V tile
-  int pipe; // software-pipelined main loop for launches without features
 };
 
 __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx) {
