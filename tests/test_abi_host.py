@@ -90,6 +90,9 @@ def _args(**kw):
     (dict(q=None), nat.TRINIX_ERR_NULL_POINTER),
     (dict(q_stride=nat.int64x4((1, 1, 1, 2))), nat.TRINIX_ERR_BAD_STRIDE),
     (dict(k_stride=nat.int64x4((8 * 64 * 128, 8 * 128, 130, 1))), nat.TRINIX_ERR_BAD_STRIDE),
+    # 16-bit K/V tiles are addressed with 32-bit in-tile offsets: key-row stride < 2^22 elements
+    (dict(k_stride=nat.int64x4((1 << 30, 1 << 22, 128, 1))), nat.TRINIX_ERR_BAD_STRIDE),
+    (dict(v_stride=nat.int64x4((1 << 30, 1 << 22, 128, 1))), nat.TRINIX_ERR_BAD_STRIDE),
     (dict(dropout_p=1.0), nat.TRINIX_ERR_BAD_ARGUMENT),
     (dict(mask_blockmap=4096), nat.TRINIX_ERR_BAD_ARGUMENT),
 ])
