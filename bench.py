@@ -116,7 +116,26 @@ def time_events(fn, iters, torch):
     return start.elapsed_time(end) / iters
 
 
-def measure(w, args, torch):
+def cold_step_ms(fn, torch, iters=10):
+    """Median ms of one step with the 256 MB MALL flushed first: a 512 MiB
+    scratch buffer is written (untimed) before each step, and only the step
+    is timed with HIP events on the launch stream."""
+    scratch = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.current_stream()
+    times = []
+    for _ in range(iters):
+        scratch.fill_(1)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(st)
+        fn()
+        end.record(st)
+        end.synchronize()
+        times.append(start.elapsed_time(end))
+    del scratch
+    return sorted(times)[len(times) // 2]
+
+
+def measure(w, args, torch, cold=False):
     from trinix_amd.workloads import make_inputs, flops
 
     inp = make_inputs(w, device="cuda")
@@ -141,7 +160,8 @@ def measure(w, args, torch):
     for _ in range(3):
         kfn()
     kms = time_events(kfn, max(args.steps, 20), torch)
-    return inp, fl, ms, kms
+    cold_ms = cold_step_ms(fn, torch) if cold else None
+    return inp, fl, ms, kms, cold_ms
 
 
 def algo_bytes(w):
@@ -211,7 +231,7 @@ def main():
 
     w = WORKLOADS[args.workload]
     dname = DTYPE_NAME[str(w.dtype)]
-    inp, fl, ms, kms = measure(w, args, torch)
+    inp, fl, ms, kms, cold_ms = measure(w, args, torch, cold=True)
     value = fl / (ms * 1e-3) / 1e12
     k_tflops = fl / (kms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[dname]
@@ -249,13 +269,15 @@ def main():
             "algorithmic_bytes": algo_bytes(w),
         },
         "native_library": str(_native.LIB_PATH) if _native.library_loaded() else None,
+        # the same step with q/k/v evicted from the 256 MB MALL before each call
+        "cold_mall": {"ms_per_step": round(cold_ms, 4), "tflops": round(fl / cold_ms / 1e9, 2)},
     }
     if args.all:
         extra = {}
         for name, wo in WORKLOADS.items():
             if name == w.name:
                 continue
-            _, f2, ms2, kms2 = measure(wo, args, torch)
+            _, f2, ms2, kms2, _ = measure(wo, args, torch)
             pk = PEAK_TFLOPS[DTYPE_NAME[str(wo.dtype)]]
             extra[name] = {"ms": round(ms2, 4), "tflops": round(f2 / ms2 / 1e9, 2),
                            "kernel_ms": round(kms2, 4), "kernel_tflops": round(f2 / kms2 / 1e9, 2),

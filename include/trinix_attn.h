@@ -24,6 +24,9 @@
  *   trinix_rope_apply          <- TritonRoPEKernel.apply / _apply_rope_pytorch
  *                                 trinix/kernels/rope_kernel.py:180-222,
  *                                 trinix/layers/embeddings/rope.py:111-134
+ *   trinix_alibi_bias          <- TritonALiBiKernel.apply / FastALiBiPositionEmbedding
+ *                                 trinix/kernels/alibi_kernel.py:8-54,93-124,
+ *                                 trinix/layers/embeddings/alibi.py:65-90
  *   trinix_attn_tile_config    <- calculate_attention_block_sizes
  *                                 trinix/kernels/utils.py:87-153
  *   trinix_attn_is_available   <- TritonAttentionKernel.is_available
@@ -131,6 +134,13 @@ int trinix_rope_apply(const void* x, const int64_t x_stride[4], void* out,
                       int32_t dtype, const void* cos, const void* sin,
                       int64_t cs_stride, const int64_t* position_ids,
                       void* stream);
+
+/* ALiBi bias, reference trinix/kernels/alibi_kernel.py:8-54:
+ *   out[h*out_stride_h + i*out_stride_i + j] = -slopes[h*slope_stride] * |i - j|
+ * for h < nheads, i, j < seqlen (< 2^24), fp32, key stride 1. */
+int trinix_alibi_bias(const float* slopes, int64_t slope_stride, int64_t nheads,
+                      int64_t seqlen, float* out, int64_t out_stride_h,
+                      int64_t out_stride_i, void* stream);
 
 /* Tile shape the library launches for (head_dim, dtype). */
 typedef struct trinix_tile_cfg {

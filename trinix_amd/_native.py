@@ -105,6 +105,7 @@ SIGNATURES = {
         [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64,
          c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "trinix_alibi_bias": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "trinix_attn_tile_config": (c_int32, [c_int64, c_int32, POINTER(TileCfg)]),
     "trinix_attn_is_available": (c_int32, []),
     "trinix_status_string": (c_char_p, [c_int32]),

@@ -83,4 +83,24 @@ class TritonRoPEKernel:
     @staticmethod
     def apply(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
               position_ids: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+        return TritonRoPEFunction.apply(q, k, cos, sin, position_ids)
+
+
+class TritonRoPEFunction(torch.autograd.Function):
+    """RoPE on q and k with the reference's backward (``rope_kernel.py:134-177``):
+    the gradient of a rotation by +theta is the rotation by -theta, i.e. the
+    same kernel with sin negated.  cos/sin receive no gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, cos, sin, position_ids=None):
+        ctx.save_for_backward(cos, sin)
+        ctx.position_ids = position_ids
         return rope_apply(q, cos, sin, position_ids), rope_apply(k, cos, sin, position_ids)
+
+    @staticmethod
+    def backward(ctx, grad_q, grad_k):
+        cos, sin = ctx.saved_tensors
+        neg = -sin
+        gq = rope_apply(grad_q, cos, neg, ctx.position_ids) if grad_q is not None else None
+        gk = rope_apply(grad_k, cos, neg, ctx.position_ids) if grad_k is not None else None
+        return gq, gk, None, None, None

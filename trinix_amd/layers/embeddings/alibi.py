@@ -1,9 +1,11 @@
 """ALiBi position bias (reference ``trinix/layers/embeddings/alibi.py``).
 
-Slopes follow ``_get_slopes`` (``alibi.py:47-63``).  ``forward`` still
-returns the materialised ``-slope * |i - j|`` bias of shape (B, H, S, S) for
-API compatibility (``alibi.py:65-90``), but the attention layers never call
-it: they pass ``slopes`` to the kernel, which adds the bias per element.
+Slopes follow ``_get_slopes`` (``alibi.py:47-63``).  ``forward`` returns the
+``-slope * |i - j|`` bias of shape (B, H, S, S) for API compatibility
+(``alibi.py:65-90``): from the HIP kernel when the slopes live on the GPU and
+``use_triton`` is set (the reference's Triton branch), else in eager torch.
+The attention layers never call it: they pass ``slopes`` to the attention
+kernel, which adds the bias per element.
 """
 import math
 
@@ -32,6 +34,14 @@ class FastALiBiPositionEmbedding(nn.Module):
         return torch.tensor(slopes, dtype=torch.float32)
 
     def forward(self, seq_len: int, batch_size: int = 1) -> torch.Tensor:
+        if self.use_triton and self.slopes.is_cuda:
+            from ...kernels.alibi_kernel import TritonALiBiKernel
+
+            if TritonALiBiKernel.is_available():
+                return TritonALiBiKernel.apply(self.slopes, batch_size, self.num_heads, seq_len)
+        return self._compute_alibi_pytorch(seq_len, batch_size)
+
+    def _compute_alibi_pytorch(self, seq_len: int, batch_size: int) -> torch.Tensor:
         pos = torch.arange(seq_len, device=self.slopes.device)
         dist = (pos.unsqueeze(0) - pos.unsqueeze(1)).abs()
         bias = -(dist.unsqueeze(0) * self.slopes.unsqueeze(1).unsqueeze(2))
