@@ -24,6 +24,10 @@
  *   trinix_rope_apply          <- TritonRoPEKernel.apply / _apply_rope_pytorch
  *                                 trinix/kernels/rope_kernel.py:180-222,
  *                                 trinix/layers/embeddings/rope.py:111-134
+ *   trinix_attn_bwd            <- no counterpart: the reference's Triton attention
+ *                                 returns a detached output (attention_kernel.py:
+ *                                 497-517); gradients of the eager path
+ *                                 (trinix/layers/attention/base.py:347-400)
  *   trinix_alibi_bias          <- TritonALiBiKernel.apply / FastALiBiPositionEmbedding
  *                                 trinix/kernels/alibi_kernel.py:8-54,93-124,
  *                                 trinix/layers/embeddings/alibi.py:65-90
@@ -134,6 +138,52 @@ int trinix_rope_apply(const void* x, const int64_t x_stride[4], void* out,
                       int32_t dtype, const void* cos, const void* sin,
                       int64_t cs_stride, const int64_t* position_ids,
                       void* stream);
+
+/* Backward of trinix_attn_fwd for bf16/fp16 without dropout.  No
+ * counterpart in the reference (its Triton attention has no backward,
+ * attention_kernel.py:497-517); the gradients are those of the eager path
+ * softmax(scale*q k^T + ALiBi + mask) v (base.py:347-400):
+ *   dv = P^T dout, dz = P*(dout v^T - rowsum(dout*out)), dq = scale*dz k,
+ *   dk = scale*dz^T q (summed over the q-heads sharing a KV head).
+ * q, k, v, out, dout and the outputs dq (like q), dk, dv (like k, v) are
+ * BSHD with d stride 1; lse is the (B, Hq, Sq) fp32 natural-log row
+ * log-sum-exp written by trinix_attn_fwd; delta is a caller-provided fp32
+ * workspace of B*Hq*Sq elements.  Scale, causal, window, ALiBi and mask
+ * arguments mean what they mean in trinix_attn_fwd_args. */
+typedef struct trinix_attn_bwd_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* out;
+  const void* dout;
+  const float* lse;
+  float* delta;
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t out_stride[4];
+  int64_t dout_stride[4];
+  int64_t dq_stride[4];
+  int64_t dk_stride[4];
+  int64_t dv_stride[4];
+  int64_t batch, seqlen_q, seqlen_k, nheads_q, nheads_kv, head_dim;
+  int32_t dtype;
+  float softmax_scale;
+  int32_t causal;
+  int32_t has_window;
+  int64_t window_left, window_right;
+  const float* alibi_slopes;
+  int64_t alibi_stride[2];
+  const void* mask;
+  int32_t mask_dtype;
+  int64_t mask_stride[4];
+  const uint8_t* mask_blockmap;
+  int64_t blockmap_stride[2];
+} trinix_attn_bwd_args;
+int trinix_attn_bwd(const trinix_attn_bwd_args* args, void* stream);
 
 /* ALiBi bias, reference trinix/kernels/alibi_kernel.py:8-54:
  *   out[h*out_stride_h + i*out_stride_i + j] = -slopes[h*slope_stride] * |i - j|

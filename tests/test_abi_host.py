@@ -41,21 +41,24 @@ def test_exports_every_declared_symbol(lib):
         assert re.search(rf"\bT {n}$", out, re.M), n
 
 
-def test_struct_layout_matches_c(lib):
-    fields = [f for f, _ in nat.AttnFwdArgs._fields_]
+@pytest.mark.parametrize("cname,pyty", [("trinix_attn_fwd_args", "AttnFwdArgs"),
+                                         ("trinix_attn_bwd_args", "AttnBwdArgs"),
+                                         ("trinix_tile_cfg", "TileCfg")])
+def test_struct_layout_matches_c(lib, cname, pyty):
+    cls = getattr(nat, pyty)
+    fields = [f for f, _ in cls._fields_]
     prog = ['#include <stdio.h>', '#include <stddef.h>', '#include "trinix_attn.h"', "int main(void){",
-            'printf("%zu\\n", sizeof(trinix_attn_fwd_args));']
-    prog += [f'printf("%zu\\n", offsetof(trinix_attn_fwd_args, {f}));' for f in fields]
-    prog += ['printf("%zu\\n", sizeof(trinix_tile_cfg));', "return 0;}"]
+            f'printf("%zu\\n", sizeof({cname}));']
+    prog += [f'printf("%zu\\n", offsetof({cname}, {f}));' for f in fields]
+    prog += ["return 0;}"]
     with tempfile.TemporaryDirectory() as d:
         src, exe = os.path.join(d, "l.c"), os.path.join(d, "l")
         open(src, "w").write("\n".join(prog))
         subprocess.run(["gcc", "-std=c99", "-I", str(INCLUDE_DIR), src, "-o", exe], check=True)
         vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split()]
-    assert vals[0] == ctypes.sizeof(nat.AttnFwdArgs)
-    for f, off in zip(fields, vals[1:-1]):
-        assert getattr(nat.AttnFwdArgs, f).offset == off, f
-    assert vals[-1] == ctypes.sizeof(nat.TileCfg)
+    assert vals[0] == ctypes.sizeof(cls)
+    for f, off in zip(fields, vals[1:]):
+        assert getattr(cls, f).offset == off, f
 
 
 def test_version_status_and_tiles(lib):

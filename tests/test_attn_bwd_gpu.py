@@ -1,0 +1,171 @@
+"""GPU tests of the attention backward (``trinix_attn_bwd`` through
+``triton_attn_func`` / the layers).  The reference's Triton attention has no
+backward; the gradients to match are those of its eager path, i.e. torch
+autograd through the oracle (``oracle/attention_oracle.py``, the restated
+``base.py:347-400``).
+
+Bar (the usual one for fused attention): with fp64 autograd of the oracle as
+the truth, the HIP gradients in bf16/fp16 must be within twice the error of
+the oracle's own bf16/fp16 autograd, plus 2e-3 of the gradient's scale."""
+import pytest
+import torch
+
+import trinix_amd as tx
+from oracle import attention_oracle as orc
+from trinix_amd import triton_attn_func
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(B, Sq, Sk, H, Hkv, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Sq, H, D, generator=g)
+    k = torch.randn(B, Sk, Hkv, D, generator=g)
+    v = torch.randn(B, Sk, Hkv, D, generator=g)
+    do = torch.randn(B, Sq, H, D, generator=g)
+    return q, k, v, do
+
+
+def _eager_grads(q, k, v, do, dtype, **kw):
+    ts = [t.to(dtype).requires_grad_(True) for t in (q, k, v)]
+    out = orc.functional_attention(*ts, **kw)
+    out.backward(do.to(dtype))
+    return out.detach().double(), [t.grad.double() for t in ts]
+
+
+def _hip_grads(q, k, v, do, dtype, **kw):
+    ts = [t.to(DEV, dtype).requires_grad_(True) for t in (q, k, v)]
+    kw = {key: (val.to(DEV) if torch.is_tensor(val) else val) for key, val in kw.items()}
+    out = triton_attn_func(*ts, **kw)
+    out.backward(do.to(DEV, dtype))
+    return out.detach().cpu().double(), [t.grad.cpu().double() for t in ts]
+
+
+def _check(hip, eager, truth):
+    for name, h, e, t in zip("qkv", hip, eager, truth):
+        scale = t.abs().max().item()
+        err_h = (h - t).abs().max().item()
+        err_e = (e - t).abs().max().item()
+        assert err_h <= 2 * err_e + 2e-3 * scale, (name, err_h, err_e, scale)
+
+
+CASES = [
+    # (B, Sq, Sk, H, Hkv, D, dtype, kwargs)
+    (2, 160, 160, 4, 4, 64, torch.bfloat16, dict()),
+    (1, 200, 200, 4, 2, 128, torch.bfloat16, dict(causal=True)),
+    (1, 256, 256, 4, 1, 128, torch.float16, dict(causal=True, window_size=(70, 0))),
+    (2, 96, 150, 2, 2, 64, torch.bfloat16, dict(softmax_scale=0.2)),
+    (1, 130, 130, 4, 2, 64, torch.float16, dict(window_size=(20, 33))),
+    (2, 128, 128, 4, 4, 64, torch.float16, dict(alibi_slopes=orc.alibi_slopes(4))),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_backward_matches_eager_autograd(case):
+    B, Sq, Sk, H, Hkv, D, dtype, kw = CASES[case]
+    q, k, v, do = _inputs(B, Sq, Sk, H, Hkv, D, seed=100 + case)
+    _, truth = _eager_grads(q, k, v, do, torch.float64, **kw)
+    _, eager = _eager_grads(q, k, v, do, dtype, **kw)
+    out, hip = _hip_grads(q, k, v, do, dtype, **kw)
+    _check(hip, eager, truth)
+
+
+def test_backward_with_block_mask_and_alibi():
+    B, S, H, D = 2, 192, 4, 64
+    q, k, v, do = _inputs(B, S, S, H, H, D, seed=7)
+    m = torch.zeros(S, S)
+    g = torch.Generator().manual_seed(3)
+    blocks = torch.rand(S // 64, S // 64, generator=g) < 0.3
+    blocks.fill_diagonal_(False)  # every row keeps its diagonal block
+    m = torch.where(blocks.repeat_interleave(64, 0).repeat_interleave(64, 1), float("-inf"), 0.0)
+    m[5, 7] = -2.5  # one finite non-zero entry: a per-element block
+    kw = dict(attn_mask=m, alibi_slopes=orc.alibi_slopes(H))
+    _, truth = _eager_grads(q, k, v, do, torch.float64, **kw)
+    _, eager = _eager_grads(q, k, v, do, torch.float16, **kw)
+    _, hip = _hip_grads(q, k, v, do, torch.float16, **kw)
+    _check(hip, eager, truth)
+
+
+def test_backward_fused_rope_and_lse_output():
+    B, S, H, Hkv, D = 1, 144, 4, 2, 128
+    q, k, v, do = _inputs(B, S, S, H, Hkv, D, seed=11)
+    dtype = torch.bfloat16
+
+    def eager(dt):
+        cos, sin = orc.rope_tables(S, D, 500000.0, dt)
+        ts = [t.to(dt).requires_grad_(True) for t in (q, k, v)]
+        out = orc.functional_attention(orc.apply_rope(ts[0], cos, sin), orc.apply_rope(ts[1], cos, sin), ts[2],
+                                       causal=True)
+        out.backward(do.to(dt))
+        return [t.grad.double() for t in ts]
+
+    truth, ref = eager(torch.float64), eager(dtype)
+    cos, sin = orc.rope_tables(S, D, 500000.0, dtype)
+    ts = [t.to(DEV, dtype).requires_grad_(True) for t in (q, k, v)]
+    out, lse = triton_attn_func(*ts, causal=True, rotary_cos=cos.to(DEV), rotary_sin=sin.to(DEV), return_lse=True)
+    assert not lse.requires_grad and lse.shape == (B, H, S)
+    out.backward(do.to(DEV, dtype))
+    _check([t.grad.cpu().double() for t in ts], ref, truth)
+
+
+def test_backward_mqa_expanded_kv_sums_over_heads():
+    B, S, H, D = 1, 100, 4, 64
+    q, k, v, do = _inputs(B, S, S, H, 1, D, seed=5)
+    qd = q.to(DEV, torch.bfloat16).requires_grad_(True)
+    kd = k.to(DEV, torch.bfloat16).requires_grad_(True)
+    vd = v.to(DEV, torch.bfloat16).requires_grad_(True)
+    out = triton_attn_func(qd, kd.expand(-1, -1, H, -1), vd.expand(-1, -1, H, -1), causal=True)
+    out.backward(do.to(DEV, torch.bfloat16))
+    _, truth = _eager_grads(q, k, v, do, torch.float64, causal=True)
+    _, eager = _eager_grads(q, k, v, do, torch.bfloat16, causal=True)
+    _check([t.grad.cpu().double() for t in (qd, kd, vd)], eager, truth)
+
+
+def test_backward_is_deterministic():
+    q, k, v, do = _inputs(1, 300, 300, 8, 2, 128, seed=9)
+    res = []
+    for _ in range(2):
+        ts = [t.to(DEV, torch.bfloat16).requires_grad_(True) for t in (q, k, v)]
+        triton_attn_func(*ts, causal=True).backward(do.to(DEV, torch.bfloat16))
+        res.append([t.grad.clone() for t in ts])
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_layer_training_step_gradients():
+    torch.manual_seed(21)
+    E, H, HKV, S = 256, 4, 2, 96
+    hip = tx.FastGroupedQueryAttention(E, H, HKV, causal=True, position_method="rope", rope_base=10000.0,
+                                       kernel_type="flash")
+    ref64 = tx.FastGroupedQueryAttention(E, H, HKV, causal=True, position_method="rope", rope_base=10000.0,
+                                         kernel_type="pytorch").double()
+    ref16 = tx.FastGroupedQueryAttention(E, H, HKV, causal=True, position_method="rope", rope_base=10000.0,
+                                         kernel_type="pytorch").to(torch.bfloat16)
+    ref64.load_state_dict(hip.state_dict())
+    ref16.load_state_dict(hip.state_dict())
+    hip = hip.to(DEV, torch.bfloat16)
+    x = torch.randn(2, S, E)
+    gy = torch.randn(2, S, E)
+    grads = []
+    for layer, dev, dt in ((hip, DEV, torch.bfloat16), (ref64, "cpu", torch.float64), (ref16, "cpu", torch.bfloat16)):
+        xi = x.to(dev, dt).requires_grad_(True)
+        y, _ = layer(xi)
+        y.backward(gy.to(dev, dt))
+        grads.append([xi.grad.cpu().double()] + [layer.get_parameter(n).grad.cpu().double()
+                                                 for n in ("q_proj.weight", "k_proj.weight", "v_proj.weight")])
+    h, t, e = grads
+    for gh, gt, ge in zip(h, t, e):
+        scale = gt.abs().max().item()
+        assert (gh - gt).abs().max().item() <= 2 * (ge - gt).abs().max().item() + 2e-3 * scale
+
+
+def test_fp32_with_grad_keeps_reference_detached_output():
+    from trinix_amd.kernels import attention_kernel as ak
+
+    ak._warned_no_grad.clear()
+    q, k, v, _ = _inputs(1, 64, 64, 2, 2, 64, seed=1)
+    ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v)]
+    with pytest.warns(UserWarning, match="detached"):
+        out = triton_attn_func(*ts)
+    assert out.grad_fn is None

@@ -81,6 +81,50 @@ class AttnFwdArgs(ctypes.Structure):
     ]
 
 
+class AttnBwdArgs(ctypes.Structure):
+    """Mirror of ``trinix_attn_bwd_args`` (field order and types identical)."""
+
+    _fields_ = [
+        ("q", c_void_p),
+        ("k", c_void_p),
+        ("v", c_void_p),
+        ("out", c_void_p),
+        ("dout", c_void_p),
+        ("lse", c_void_p),
+        ("delta", c_void_p),
+        ("dq", c_void_p),
+        ("dk", c_void_p),
+        ("dv", c_void_p),
+        ("q_stride", Int64x4),
+        ("k_stride", Int64x4),
+        ("v_stride", Int64x4),
+        ("out_stride", Int64x4),
+        ("dout_stride", Int64x4),
+        ("dq_stride", Int64x4),
+        ("dk_stride", Int64x4),
+        ("dv_stride", Int64x4),
+        ("batch", c_int64),
+        ("seqlen_q", c_int64),
+        ("seqlen_k", c_int64),
+        ("nheads_q", c_int64),
+        ("nheads_kv", c_int64),
+        ("head_dim", c_int64),
+        ("dtype", c_int32),
+        ("softmax_scale", c_float),
+        ("causal", c_int32),
+        ("has_window", c_int32),
+        ("window_left", c_int64),
+        ("window_right", c_int64),
+        ("alibi_slopes", c_void_p),
+        ("alibi_stride", Int64x2),
+        ("mask", c_void_p),
+        ("mask_dtype", c_int32),
+        ("mask_stride", Int64x4),
+        ("mask_blockmap", c_void_p),
+        ("blockmap_stride", Int64x2),
+    ]
+
+
 class TileCfg(ctypes.Structure):
     """Mirror of ``trinix_tile_cfg``."""
 
@@ -105,6 +149,7 @@ SIGNATURES = {
         [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64,
          c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "trinix_attn_bwd": (c_int32, [POINTER(AttnBwdArgs), c_void_p]),
     "trinix_alibi_bias": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "trinix_attn_tile_config": (c_int32, [c_int64, c_int32, POINTER(TileCfg)]),
     "trinix_attn_is_available": (c_int32, []),

@@ -1,0 +1,147 @@
+// Host entry point of the attention backward (C ABI) and the delta pre-pass.
+//
+// trinix_attn_bwd validates the arguments, computes delta = rowsum(dO * O)
+// into the caller's workspace and launches the dK/dV and dQ kernels
+// (attn_bwd16.h, instantiated per (dtype, head_dim) in attn_bwd16_*.hip).
+#include <cstdint>
+
+#include "attn_bwd16.h"
+
+namespace trinix {
+namespace {
+
+// delta[(b*Hq + h)*Sq + i] = sum_d dO[b,i,h,d] * O[b,i,h,d] in fp32; D/8 lanes
+// per row, one 16-byte chunk each, reduced across the lanes of the row.
+template <class E, int D>
+__global__ __launch_bounds__(256) void bwd_delta_kernel(const uint16_t* __restrict__ o, int64_t o_sb, int64_t o_ss,
+                                                        int64_t o_sh, const uint16_t* __restrict__ dout, int64_t do_sb,
+                                                        int64_t do_ss, int64_t do_sh, float* __restrict__ delta, int Hq,
+                                                        int Sq, int64_t rows) {
+  constexpr int LPR = D / 8, RPB = 256 / LPR;
+  const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int t = threadIdx.x % LPR;
+  float acc = 0.f;
+  if (row < rows) {
+    const int i = (int)(row % Sq);
+    const int64_t bh = row / Sq;
+    const int h = (int)(bh % Hq);
+    const int64_t b = bh / Hq;
+    const u32x4_t ov = *(const u32x4_t*)(o + b * o_sb + i * o_ss + h * o_sh + t * 8);
+    const u32x4_t dv = *(const u32x4_t*)(dout + b * do_sb + i * do_ss + h * do_sh + t * 8);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc += E::lo(ov[e]) * E::lo(dv[e]) + E::hi(ov[e]) * E::hi(dv[e]);
+  }
+#pragma unroll
+  for (int m = LPR / 2; m >= 1; m /= 2) acc += __shfl_xor(acc, m);
+  if (t == 0 && row < rows) delta[row] = acc;
+}
+
+template <class E, int D>
+void launch_delta(const BwdParams& p, hipStream_t st) {
+  constexpr int RPB = 256 / (D / 8);
+  const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
+  hipLaunchKernelGGL((bwd_delta_kernel<E, D>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st, p.o,
+                     p.o_sb, p.o_ss, p.o_sh, p.dout, p.do_sb, p.do_ss, p.do_sh, p.delta, p.Hq, p.Sq, rows);
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+// 16-bit BSHD tensor: head_dim stride 1, 16-byte aligned rows, and a row
+// stride the 32-bit in-tile offsets can address (tiles of up to 128 rows).
+int check16(const void* ptr, const int64_t st[4]) {
+  if (!ptr) return TRINIX_ERR_NULL_POINTER;
+  if (st[3] != 1 || !aligned16(ptr)) return TRINIX_ERR_BAD_STRIDE;
+  for (int a = 0; a < 3; ++a)
+    if (st[a] % 8 != 0) return TRINIX_ERR_BAD_STRIDE;
+  if (st[1] < 0 || st[1] >= (1ll << 22)) return TRINIX_ERR_BAD_STRIDE;
+  return TRINIX_OK;
+}
+
+}  // namespace
+}  // namespace trinix
+
+using namespace trinix;
+
+extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
+  if (!a) return TRINIX_ERR_NULL_POINTER;
+  if (a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0 ||
+      a->nheads_q % a->nheads_kv != 0)
+    return TRINIX_ERR_BAD_SHAPE;
+  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
+    return TRINIX_ERR_BAD_SHAPE;
+  if (!a->lse || !a->delta) return TRINIX_ERR_NULL_POINTER;
+  int rc;
+  if ((rc = check16(a->q, a->q_stride)) || (rc = check16(a->k, a->k_stride)) || (rc = check16(a->v, a->v_stride)) ||
+      (rc = check16(a->out, a->out_stride)) || (rc = check16(a->dout, a->dout_stride)) ||
+      (rc = check16(a->dq, a->dq_stride)) || (rc = check16(a->dk, a->dk_stride)) ||
+      (rc = check16(a->dv, a->dv_stride)))
+    return rc;
+  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
+      a->mask_dtype != TRINIX_U8)
+    return TRINIX_ERR_BAD_DTYPE;
+  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+
+  BwdParams p;
+  p.q = (const uint16_t*)a->q;
+  p.k = (const uint16_t*)a->k;
+  p.v = (const uint16_t*)a->v;
+  p.o = (const uint16_t*)a->out;
+  p.dout = (const uint16_t*)a->dout;
+  p.lse = a->lse;
+  p.delta = a->delta;
+  p.dq = (uint16_t*)a->dq;
+  p.dk = (uint16_t*)a->dk;
+  p.dv = (uint16_t*)a->dv;
+  p.q_sb = a->q_stride[0]; p.q_ss = a->q_stride[1]; p.q_sh = a->q_stride[2];
+  p.k_sb = a->k_stride[0]; p.k_ss = a->k_stride[1]; p.k_sh = a->k_stride[2];
+  p.v_sb = a->v_stride[0]; p.v_ss = a->v_stride[1]; p.v_sh = a->v_stride[2];
+  p.o_sb = a->out_stride[0]; p.o_ss = a->out_stride[1]; p.o_sh = a->out_stride[2];
+  p.do_sb = a->dout_stride[0]; p.do_ss = a->dout_stride[1]; p.do_sh = a->dout_stride[2];
+  p.dq_sb = a->dq_stride[0]; p.dq_ss = a->dq_stride[1]; p.dq_sh = a->dq_stride[2];
+  p.dk_sb = a->dk_stride[0]; p.dk_ss = a->dk_stride[1]; p.dk_sh = a->dk_stride[2];
+  p.dv_sb = a->dv_stride[0]; p.dv_ss = a->dv_stride[1]; p.dv_sh = a->dv_stride[2];
+  p.B = (int)a->batch;
+  p.Sq = (int)a->seqlen_q;
+  p.Sk = (int)a->seqlen_k;
+  p.Hq = (int)a->nheads_q;
+  p.Hkv = (int)a->nheads_kv;
+  p.G = p.Hq / p.Hkv;
+  p.scale = a->softmax_scale;
+  p.scale_log2 = a->softmax_scale * kLog2e;
+  p.causal = a->causal ? 1 : 0;
+  p.has_window = a->has_window ? 1 : 0;
+  p.wl = a->window_left;
+  p.wr = a->window_right;
+  p.alibi = a->alibi_slopes;
+  p.al_sb = a->alibi_stride[0];
+  p.al_sh = a->alibi_stride[1];
+  p.mask = a->mask;
+  p.mask_dtype = a->mask_dtype;
+  p.mk_sb = a->mask_stride[0]; p.mk_sh = a->mask_stride[1]; p.mk_si = a->mask_stride[2]; p.mk_sj = a->mask_stride[3];
+  p.bmap = a->mask_blockmap;
+  p.bm_sb = a->blockmap_stride[0];
+  p.bm_sh = a->blockmap_stride[1];
+  p.bm_cols = (int)((a->seqlen_k + 63) / 64);
+  p.num_kblk = (int)((a->seqlen_k + 127) / 128);
+  p.num_mblk = (int)((a->seqlen_q + 127) / 128);
+  if ((int64_t)p.B * p.Hq * p.num_mblk >= (1ll << 31) || (int64_t)p.B * p.Hkv * p.num_kblk >= (1ll << 31))
+    return TRINIX_ERR_BAD_SHAPE;
+  const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0);
+
+  hipStream_t st = (hipStream_t)stream;
+  (void)hipGetLastError();
+  hipError_t err;
+  const bool bf = a->dtype == TRINIX_BF16;
+  if (a->head_dim == 128) {
+    if (bf) launch_delta<BF16, 128>(p, st);
+    else launch_delta<F16, 128>(p, st);
+    err = bf ? launch_bwd16_bf16_d128(p, feat, st) : launch_bwd16_f16_d128(p, feat, st);
+  } else {
+    if (bf) launch_delta<BF16, 64>(p, st);
+    else launch_delta<F16, 64>(p, st);
+    err = bf ? launch_bwd16_bf16_d64(p, feat, st) : launch_bwd16_f16_d64(p, feat, st);
+  }
+  return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+}

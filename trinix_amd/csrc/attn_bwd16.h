@@ -1,0 +1,529 @@
+// Backward of the bf16/fp16 attention forward (head_dim 64/128), from the
+// log-sum-exp the forward saves.  No counterpart in the reference: its
+// Triton path returns a detached output (trinix/kernels/attention_kernel.py:
+// 497-517); the gradients follow the eager path's softmax(scale*q k^T +
+// bias + mask) v (trinix/layers/attention/base.py:347-400).
+//
+// With z = scale*q.k (+ ALiBi + mask), P = exp(z - lse), O = P V:
+//   dV = P^T dO,  dP = dO V^T,  dZ = P * (dP - delta),  delta = rowsum(dO*O),
+//   dK = scale * dZ^T Q,  dQ = scale * dZ K.
+// Three launches, no atomics (deterministic):
+//   bwd_delta  delta[b, h, i] = sum_d dO*O (fp32);
+//   bwd_dkdv   one workgroup per (batch, kv-head, 128 keys): each wavefront
+//              keeps its 32 keys' K and V rows in registers and walks every
+//              q-head of its group and every query tile of the band, so dK
+//              and dV of a KV head are summed in registers (GQA included);
+//   bwd_dq     one workgroup per (batch, q-head, 128 query rows), the
+//              forward's shape: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
+// All products run on v_mfma_f32_32x32x16_{bf16,f16}; P and dZ are rounded to
+// the input dtype for their products, as in the forward.
+#pragma once
+#include <climits>
+
+#include "attn_params.h"
+#include "lds_tile.h"
+
+namespace trinix {
+
+struct BwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  const float* lse;  // (B, Hq, Sq), natural log
+  float* delta;      // (B, Hq, Sq)
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t q_sb, q_ss, q_sh, k_sb, k_ss, k_sh, v_sb, v_ss, v_sh;
+  int64_t o_sb, o_ss, o_sh, do_sb, do_ss, do_sh;
+  int64_t dq_sb, dq_ss, dq_sh, dk_sb, dk_ss, dk_sh, dv_sb, dv_ss, dv_sh;
+  int B, Sq, Sk, Hq, Hkv, G;
+  float scale, scale_log2;
+  int causal, has_window;
+  int64_t wl, wr;
+  const float* alibi;
+  int64_t al_sb, al_sh;
+  const void* mask;
+  int mask_dtype;
+  int64_t mk_sb, mk_sh, mk_si, mk_sj;
+  const uint8_t* bmap;
+  int64_t bm_sb, bm_sh;
+  int bm_cols;
+  int num_kblk, num_mblk;  // 128-key blocks (dK/dV), 128-row blocks (dQ)
+};
+
+// Allowed (i, j): j - i in [dlo, dhi] (causal: j <= i; window: -wl <= j-i <= wr).
+struct Band {
+  int dlo, dhi;
+  __device__ Band(const BwdParams& p) {
+    int64_t lo = INT_MIN / 2, hi = INT_MAX / 2;
+    if (p.causal) hi = 0;
+    if (p.has_window) {
+      lo = lo > -p.wl ? lo : -p.wl;
+      hi = hi < p.wr ? hi : p.wr;
+    }
+    dlo = (int)(lo < INT_MIN / 2 ? INT_MIN / 2 : lo);
+    dhi = (int)(hi > INT_MAX / 2 ? INT_MAX / 2 : hi);
+  }
+  __device__ bool ok(int i, int j) const { return j - i >= dlo && j - i <= dhi; }
+};
+
+// ---------------------------------------------------------------------------
+// dK, dV.  Lane l of wavefront w owns key j = kb0 + 32w + l%32.  Per 32-query
+// sub-tile: S = Q K^T and dP = dO V^T with the query rows on the MFMA rows
+// (A operand: Q / dO rows read from LDS) and keys on the columns (B operand:
+// the lane's K / V row in registers), so S, dP, P and dZ of a lane are its
+// key's column; dV^T += dO^T P and dK^T += Q^T dZ take P / dZ straight from
+// those registers as the B operand and dO^T / Q^T through LDS transpose reads.
+// ---------------------------------------------------------------------------
+template <class E, int D, bool ALIBI, bool MASK>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
+  constexpr int NW = 4, BK = NW * 32, BQ = 64;
+  constexpr int DS = D / 16, DB = D / 32, UPR = D / 8;
+  constexpr int LPW = BQ * UPR / (64 * NW);  // 16-byte copies per wavefront per Q (or dO) tile
+  static_assert(LPW >= 1 && BQ * UPR % (64 * NW) == 0, "tile shape");
+
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_q0[BQ * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_q1[BQ * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_o0[BQ * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_o1[BQ * D];
+  __shared__ __attribute__((aligned(256))) float lds_l0[BQ];
+  __shared__ __attribute__((aligned(256))) float lds_l1[BQ];
+  __shared__ __attribute__((aligned(256))) float lds_d0[BQ];
+  __shared__ __attribute__((aligned(256))) float lds_d1[BQ];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, g = lane >> 5;
+
+  int w = xcd_remap(blockIdx.x, p.B * p.Hkv * p.num_kblk);
+  const int kblk = w % p.num_kblk;  // causal: low key blocks see the most queries, and run first
+  w /= p.num_kblk;
+  const int hkv = w % p.Hkv;
+  const int b = w / p.Hkv;
+  const int kb0 = kblk * BK;
+  const int j0 = kb0 + wave * 32;
+  const int j = j0 + r;
+  const int jc = min(j, p.Sk - 1);
+  const Band band(p);
+  const float c = p.scale_log2;
+
+  // this lane's K and V rows (B operands of S and dP)
+  u32x4_t kr[DS], vr[DS];
+  {
+    const uint16_t* krow = p.k + b * p.k_sb + hkv * p.k_sh + (int64_t)jc * p.k_ss;
+    const uint16_t* vrow = p.v + b * p.v_sb + hkv * p.v_sh + (int64_t)jc * p.v_ss;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      kr[ds] = *(const u32x4_t*)(krow + ds * 16 + g * 8);
+      vr[ds] = *(const u32x4_t*)(vrow + ds * 16 + g * 8);
+    }
+  }
+  f32x16_t dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dk[db] = dv[db] = (f32x16_t){};
+
+  // Query range of the workgroup's keys [kb0, kb0 + BK): i - j in [-dhi, -dlo].
+  const int kmax = min(kb0 + BK, p.Sk) - 1;
+  int i_lo = (int)max((int64_t)0, (int64_t)kb0 - band.dhi);
+  int i_hi = (int)min((int64_t)p.Sq, (int64_t)kmax - band.dlo + 1);
+  const int qt_lo = i_lo / BQ;
+  const int qt_hi = i_hi > i_lo ? (i_hi + BQ - 1) / BQ : qt_lo;
+  const int nqt = qt_hi - qt_lo;
+
+  // ---- tile copies: Q and dO rows (16-byte units, swizzled), lse and delta
+  auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
+  auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_k<D>(ld_row(l)); };
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
+  auto load_rows = [&](const uint16_t* base, int64_t ss, uint16_t* lds_tile, int i0) __attribute__((always_inline)) {
+    const uint64_t gb = uniform_ptr((const char*)base + (int64_t)i0 * ss * 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds_tile + wave_lds;
+    const int last = p.Sq - 1 - i0;  // rows past Sq load row Sq-1 (finite, masked out)
+#pragma unroll
+    for (int l = 0; l < LPW; ++l) {
+      const uint32_t row = (uint32_t)min(ld_row(l), last);
+      dma_16b_s(row * (uint32_t)ss * 2u + (uint32_t)ld_unit(l) * 16u, gb,
+                __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
+    }
+  };
+  auto load_vec = [&](const float* base, float* lds_vec, int i0) __attribute__((always_inline)) {
+    const uint64_t gb = uniform_ptr(base + i0);
+    const uint32_t row = (uint32_t)min(lane, p.Sq - 1 - i0);
+    dma_4b_s(row * 4u, gb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_vec));
+  };
+  auto load_tile = [&](auto slot_c, int hq, int qt) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot_c)::value;
+    const int i0 = qt * BQ;
+    load_rows(p.q + b * p.q_sb + hq * p.q_sh, p.q_ss, SL ? lds_q1 : lds_q0, i0);
+    load_rows(p.dout + b * p.do_sb + hq * p.do_sh, p.do_ss, SL ? lds_o1 : lds_o0, i0);
+    const int64_t vo = ((int64_t)b * p.Hq + hq) * p.Sq;
+    if (wave == 0) load_vec(p.lse + vo, SL ? lds_l1 : lds_l0, i0);
+    if (wave == 1) load_vec(p.delta + vo, SL ? lds_d1 : lds_d0, i0);
+  };
+
+  // ---- LDS operand reads of a Q / dO tile (rows swizzled with swz_k)
+  // Row read (A operand of S / dP): query row qrow, head_dim chunk ds.
+  auto rowread = [&](const uint16_t* tile, int qrow, int ds) __attribute__((always_inline)) {
+    const int unit = (ds * 2 + g) ^ swz_k<D>(qrow);
+    return *(const u32x4_t*)(tile + qrow * D + unit * 8);
+  };
+  // Transpose read (A operand of dV^T / dK^T): head_dim rows db*32 + l%32,
+  // the 8 queries of k-group g of k-step kk of sub-tile st (queries
+  // st*32 + kk*16 + {4g..4g+3, 8+4g..8+4g+3}, matching P's register rows).
+  const int tr_G = lane >> 4, tr_s = lane & 15, tr_g = tr_G >> 1, tr_dh = tr_G & 1;
+  auto trread = [&](const uint16_t* tile, int st, int db, int kk) __attribute__((always_inline)) {
+    const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);
+    const int half = (tr_s & 1) * 4;
+    const int row0 = st * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
+    const int row1 = row0 + 8;
+    const s16x4_t lo4 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_k<D>(row0)) * 8 + half));
+    const s16x4_t hi4 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_k<D>(row1)) * 8 + half));
+    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
+    return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
+  };
+
+  // ---- one 32-query sub-tile against this wavefront's 32 keys
+  auto subtile = [&](auto pred_c, const uint16_t* qt_lds, const uint16_t* ot_lds, const float* l_lds,
+                     const float* d_lds, int st, int i0, int hq, float slope_l2, int mcode) __attribute__((always_inline)) {
+    constexpr bool PRED = decltype(pred_c)::value;
+    f32x16_t s = {}, dp = {};
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) s = E::mfma(rowread(qt_lds, st * 32 + r, ds), kr[ds], s);
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) dp = E::mfma(rowread(ot_lds, st * 32 + r, ds), vr[ds], dp);
+    // element v of the lane: query row st*32 + (v/4)*8 + 4g + v%4 of the tile
+    const char* mrow = nullptr;
+    if constexpr (MASK) {
+      if (mcode > 0) {
+        const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
+        mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)jc * p.mk_sj) * esz;
+      }
+    }
+    float pv[16], dz[16];
+#pragma unroll
+    for (int vq = 0; vq < 4; ++vq) {
+      const f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
+      const f32x4_t d4 = *(const f32x4_t*)(d_lds + st * 32 + vq * 8 + g * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int v = vq * 4 + e;
+        const int i = i0 + st * 32 + vq * 8 + g * 4 + e;
+        float x = s[v] * c;
+        if constexpr (ALIBI) x += slope_l2 * (float)abs(i - j);
+        if constexpr (MASK) {
+          if (mcode > 0 && i < p.Sq) x += load_mask_elem(mrow, p.mask_dtype, (int64_t)i * p.mk_si) * kLog2e;
+        }
+        if constexpr (PRED) x = (band.ok(i, j) && i < p.Sq && j < p.Sk) ? x : -INFINITY;
+        const float pe = __builtin_amdgcn_exp2f(x - l4[e] * kLog2e);
+        pv[v] = pe;
+        dz[v] = pe * (dp[v] - d4[e]);
+      }
+    }
+    u32x4_t pb[2], zb[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      pb[kk] = (u32x4_t){E::pack(pv[kk * 8 + 0], pv[kk * 8 + 1]), E::pack(pv[kk * 8 + 2], pv[kk * 8 + 3]),
+                         E::pack(pv[kk * 8 + 4], pv[kk * 8 + 5]), E::pack(pv[kk * 8 + 6], pv[kk * 8 + 7])};
+      zb[kk] = (u32x4_t){E::pack(dz[kk * 8 + 0], dz[kk * 8 + 1]), E::pack(dz[kk * 8 + 2], dz[kk * 8 + 3]),
+                         E::pack(dz[kk * 8 + 4], dz[kk * 8 + 5]), E::pack(dz[kk * 8 + 6], dz[kk * 8 + 7])};
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        dv[db] = E::mfma(trread(ot_lds, st, db, kk), pb[kk], dv[db]);
+        dk[db] = E::mfma(trread(qt_lds, st, db, kk), zb[kk], dk[db]);
+      }
+  };
+
+  // ---- walk the q-heads of the group and the query tiles of the band
+  for (int gh = 0; gh < p.G; ++gh) {
+    const int hq = hkv * p.G + gh;
+    float slope_l2 = 0.f;
+    if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
+    if (nqt <= 0) break;
+    __syncthreads();  // the previous head's last tile is no longer read
+    load_tile(std::integral_constant<int, 0>{}, hq, qt_lo);
+    auto step = [&](auto slot_c, int qt) __attribute__((always_inline)) {
+      constexpr int SL = decltype(slot_c)::value;
+      __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of tile qt landed
+      __syncthreads();                // ... and every wavefront's; tile qt-1 is no longer read
+      if (qt + 1 < qt_hi) load_tile(std::integral_constant<int, 1 - SL>{}, hq, qt + 1);
+      const uint16_t* qt_lds = SL ? lds_q1 : lds_q0;
+      const uint16_t* ot_lds = SL ? lds_o1 : lds_o0;
+      const float* l_lds = SL ? lds_l1 : lds_l0;
+      const float* d_lds = SL ? lds_d1 : lds_d0;
+#pragma unroll
+      for (int st = 0; st < BQ / 32; ++st) {
+        const int i0 = qt * BQ;
+        const int ia = i0 + st * 32, ib = min(ia + 31, p.Sq - 1);
+        if (ia >= p.Sq || j0 >= p.Sk) continue;
+        // pairs (i in [ia, ib], j in [j0, j0+31]) with j - i in [dlo, dhi]
+        const int jb = min(j0 + 31, p.Sk - 1);
+        if (j0 - ib > band.dhi || jb - ia < band.dlo) continue;  // nothing allowed
+        int mcode = 1;
+        if constexpr (MASK) {
+          if (p.bmap) {
+            const uint8_t code = p.bmap[b * p.bm_sb + hq * p.bm_sh + (int64_t)(ia / 32) * p.bm_cols + j0 / 64];
+            if (code == 2) continue;
+            mcode = code == 0 ? 0 : 1;
+          }
+        }
+        const bool full = ia + 31 < p.Sq && j0 + 31 < p.Sk && jb - ia <= band.dhi && j0 - ib >= band.dlo;
+        if (full) subtile(std::false_type{}, qt_lds, ot_lds, l_lds, d_lds, st, i0, hq, slope_l2, mcode);
+        else subtile(std::true_type{}, qt_lds, ot_lds, l_lds, d_lds, st, i0, hq, slope_l2, mcode);
+      }
+    };
+    int qt = qt_lo;
+    for (; qt + 1 < qt_hi; qt += 2) {
+      step(std::integral_constant<int, 0>{}, qt);
+      step(std::integral_constant<int, 1>{}, qt + 1);
+    }
+    if (qt < qt_hi) step(std::integral_constant<int, 0>{}, qt);
+  }
+
+  // ---- epilogue: dK = scale * dZ^T Q, dV; lane row = key j, d = db*32 + vq*8 + 4g + e
+  if (j < p.Sk) {
+    uint16_t* dkrow = p.dk + b * p.dk_sb + hkv * p.dk_sh + (int64_t)j * p.dk_ss;
+    uint16_t* dvrow = p.dv + b * p.dv_sb + hkv * p.dv_sh + (int64_t)j * p.dv_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int vq = 0; vq < 4; ++vq) {
+        const int d0 = db * 32 + vq * 8 + g * 4;
+        *(u32x2_t*)(dkrow + d0) = (u32x2_t){E::pack(dk[db][vq * 4 + 0] * p.scale, dk[db][vq * 4 + 1] * p.scale),
+                                            E::pack(dk[db][vq * 4 + 2] * p.scale, dk[db][vq * 4 + 3] * p.scale)};
+        *(u32x2_t*)(dvrow + d0) = (u32x2_t){E::pack(dv[db][vq * 4 + 0], dv[db][vq * 4 + 1]),
+                                            E::pack(dv[db][vq * 4 + 2], dv[db][vq * 4 + 3])};
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ.  The forward's decomposition: lane l of wavefront w owns query row
+// i = m0 + 32w + l%32; per 64-key tile S^T = K Q^T and dP^T = V dO^T (keys on
+// the MFMA rows, A operands from the K / V tiles in LDS; B operands the
+// lane's Q / dO rows in registers), dZ^T = P^T (dP^T - delta) in registers,
+// dQ^T += K^T dZ^T with K^T from LDS transpose reads.
+// ---------------------------------------------------------------------------
+template <class E, int D, bool ALIBI, bool MASK>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
+  constexpr int NW = 4, BM = NW * 32, BN = 64;
+  constexpr int DS = D / 16, DB = D / 32, NB = BN / 32, UPR = D / 8;
+  constexpr int LPW = BN * UPR / (64 * NW);
+
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k0[BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[BN * D];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 31, g = lane >> 5;
+
+  int w = xcd_remap(blockIdx.x, p.B * p.Hq * p.num_mblk);
+  const int gq = w % p.G;
+  w /= p.G;
+  const int mi = w % p.num_mblk;
+  w /= p.num_mblk;
+  const int hkv = w % p.Hkv;
+  const int b = w / p.Hkv;
+  const int hq = hkv * p.G + gq;
+  const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
+  const int m0 = mblk * BM;
+  const int iw0 = m0 + wave * 32;
+  const int i = iw0 + r;
+  const int ic = min(i, p.Sq - 1);
+  const Band band(p);
+  const float c = p.scale_log2;
+
+  u32x4_t qr[DS], dor[DS];
+  {
+    const uint16_t* qrow = p.q + b * p.q_sb + hq * p.q_sh + (int64_t)ic * p.q_ss;
+    const uint16_t* orow = p.dout + b * p.do_sb + hq * p.do_sh + (int64_t)ic * p.do_ss;
+#pragma unroll
+    for (int ds = 0; ds < DS; ++ds) {
+      qr[ds] = *(const u32x4_t*)(qrow + ds * 16 + g * 8);
+      dor[ds] = *(const u32x4_t*)(orow + ds * 16 + g * 8);
+    }
+  }
+  const int64_t vo = ((int64_t)b * p.Hq + hq) * p.Sq + ic;
+  const float lse2 = p.lse[vo] * kLog2e;
+  const float dlt = p.delta[vo];
+  float slope_l2 = 0.f;
+  if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
+  const char* mrow = nullptr;
+  if constexpr (MASK) {
+    const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
+    mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)ic * p.mk_si) * esz;
+  }
+  f32x16_t acc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) acc[db] = (f32x16_t){};
+
+  // key tiles of the band of rows [m0, m0 + BM): j - i in [dlo, dhi]
+  const int mlast = min(m0 + BM, p.Sq) - 1;
+  const int64_t lo = max((int64_t)0, (int64_t)m0 + band.dlo);
+  const int64_t hi = min((int64_t)p.Sk, (int64_t)mlast + band.dhi + 1);
+  const int t_lo = (int)(lo / BN);
+  const int t_hi = hi > lo ? (int)((hi + BN - 1) / BN) : t_lo;
+
+  const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
+  const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
+  auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
+  auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_k<D>(ld_row(l)); };
+  const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
+  auto load_rows = [&](const uint16_t* base, int64_t ss, uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
+    const int n0 = tile * BN;
+    const uint64_t gb = uniform_ptr((const char*)base + (int64_t)n0 * ss * 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_void_t*)lds_tile + wave_lds;
+    const int last = p.Sk - 1 - n0;
+#pragma unroll
+    for (int l = 0; l < LPW; ++l) {
+      const uint32_t row = (uint32_t)min(ld_row(l), last);
+      dma_16b_s(row * (uint32_t)ss * 2u + (uint32_t)ld_unit(l) * 16u, gb,
+                __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
+    }
+  };
+  auto rowread = [&](const uint16_t* tile, int krow, int ds) __attribute__((always_inline)) {
+    const int unit = (ds * 2 + g) ^ swz_k<D>(krow);
+    return *(const u32x4_t*)(tile + krow * D + unit * 8);
+  };
+  const int tr_G = lane >> 4, tr_s = lane & 15, tr_g = tr_G >> 1, tr_dh = tr_G & 1;
+  auto trread = [&](const uint16_t* tile, int nb, int db, int kk) __attribute__((always_inline)) {
+    const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);
+    const int half = (tr_s & 1) * 4;
+    const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
+    const int row1 = row0 + 8;
+    const s16x4_t lo4 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_k<D>(row0)) * 8 + half));
+    const s16x4_t hi4 =
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_k<D>(row1)) * 8 + half));
+    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
+    return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
+  };
+
+  auto tile_body = [&](auto pred_c, const uint16_t* kt, const uint16_t* vt, int t) __attribute__((always_inline)) {
+    constexpr bool PRED = decltype(pred_c)::value;
+    const int n0 = t * BN;
+    int mcode = 1;
+    if constexpr (MASK) {
+      if (p.bmap) {
+        const uint8_t code = p.bmap[b * p.bm_sb + hq * p.bm_sh + (int64_t)(iw0 / 32) * p.bm_cols + n0 / 64];
+        if (code == 2) return;
+        mcode = code == 0 ? 0 : 1;
+      }
+    }
+    f32x16_t s[NB], dp[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      s[nb] = dp[nb] = (f32x16_t){};
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) s[nb] = E::mfma(rowread(kt, nb * 32 + r, ds), qr[ds], s[nb]);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) dp[nb] = E::mfma(rowread(vt, nb * 32 + r, ds), dor[ds], dp[nb]);
+    }
+    u32x4_t zb[NB][2];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float z[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+        float x = s[nb][v] * c;
+        if constexpr (ALIBI) x += slope_l2 * (float)abs(i - jj);
+        if constexpr (MASK) {
+          if (mcode > 0 && jj < p.Sk) x += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
+        }
+        if constexpr (PRED) x = (band.ok(i, jj) && jj < p.Sk && i < p.Sq) ? x : -INFINITY;
+        const float pe = __builtin_amdgcn_exp2f(x - lse2);
+        z[v] = pe * (dp[nb][v] - dlt);
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        zb[nb][kk] = (u32x4_t){E::pack(z[kk * 8 + 0], z[kk * 8 + 1]), E::pack(z[kk * 8 + 2], z[kk * 8 + 3]),
+                               E::pack(z[kk * 8 + 4], z[kk * 8 + 5]), E::pack(z[kk * 8 + 6], z[kk * 8 + 7])};
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) acc[db] = E::mfma(trread(kt, nb, db, kk), zb[nb][kk], acc[db]);
+  };
+
+  if (t_lo < t_hi) {
+    load_rows(kbase, p.k_ss, lds_k0, t_lo);
+    load_rows(vbase, p.v_ss, lds_v0, t_lo);
+  }
+  const bool wave_live = iw0 < p.Sq;
+  auto step = [&](auto slot_c, int t) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slot_c)::value;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < t_hi) {
+      load_rows(kbase, p.k_ss, SL ? lds_k0 : lds_k1, t + 1);
+      load_rows(vbase, p.v_ss, SL ? lds_v0 : lds_v1, t + 1);
+    }
+    const uint16_t* kt = SL ? lds_k1 : lds_k0;
+    const uint16_t* vt = SL ? lds_v1 : lds_v0;
+    const int n0 = t * BN;
+    const int iwl = min(iw0 + 31, p.Sq - 1);
+    const int nl = min(n0 + BN, p.Sk) - 1;
+    if (!wave_live || n0 - iwl > band.dhi || nl - iw0 < band.dlo) return;  // no allowed pair
+    const bool full = iw0 + 31 < p.Sq && n0 + BN <= p.Sk && nl - iw0 <= band.dhi && n0 - iwl >= band.dlo;
+    if (full) tile_body(std::false_type{}, kt, vt, t);
+    else tile_body(std::true_type{}, kt, vt, t);
+  };
+  int t = t_lo;
+  for (; t + 1 < t_hi; t += 2) {
+    step(std::integral_constant<int, 0>{}, t);
+    step(std::integral_constant<int, 1>{}, t + 1);
+  }
+  if (t < t_hi) step(std::integral_constant<int, 0>{}, t);
+
+  if (i < p.Sq) {
+    uint16_t* qrow = p.dq + b * p.dq_sb + hq * p.dq_sh + (int64_t)i * p.dq_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int vq = 0; vq < 4; ++vq) {
+        const int d0 = db * 32 + vq * 8 + g * 4;
+        *(u32x2_t*)(qrow + d0) = (u32x2_t){E::pack(acc[db][vq * 4 + 0] * p.scale, acc[db][vq * 4 + 1] * p.scale),
+                                           E::pack(acc[db][vq * 4 + 2] * p.scale, acc[db][vq * 4 + 3] * p.scale)};
+      }
+  }
+}
+
+// Launch of both gradient kernels for one (dtype, D); feat = kFeatAlibi | kFeatMask.
+template <class E, int D>
+hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
+  const dim3 g_kv((unsigned)(p.B * p.Hkv * p.num_kblk)), g_q((unsigned)(p.B * p.Hq * p.num_mblk)), blk(256);
+  switch (feat & 3) {
+#define TRINIX_BWD_CASE(F)                                                                                        \
+  case F:                                                                                                         \
+    hipLaunchKernelGGL((attn_bwd_dkdv<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_kv, blk, 0, st, p); \
+    hipLaunchKernelGGL((attn_bwd_dq<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_q, blk, 0, st, p);    \
+    return hipGetLastError();
+    TRINIX_BWD_CASE(0)
+    TRINIX_BWD_CASE(1)
+    TRINIX_BWD_CASE(2)
+    TRINIX_BWD_CASE(3)
+#undef TRINIX_BWD_CASE
+  }
+  return hipErrorInvalidValue;
+}
+
+#define TRINIX_ATTN_BWD16_LAUNCHER(NAME, E, D) \
+  hipError_t NAME(const BwdParams& p, int feat, hipStream_t st) { return launch_bwd<E, D>(p, feat, st); }
+
+hipError_t launch_bwd16_bf16_d64(const BwdParams& p, int feat, hipStream_t st);
+hipError_t launch_bwd16_bf16_d128(const BwdParams& p, int feat, hipStream_t st);
+hipError_t launch_bwd16_f16_d64(const BwdParams& p, int feat, hipStream_t st);
+hipError_t launch_bwd16_f16_d128(const BwdParams& p, int feat, hipStream_t st);
+
+}  // namespace trinix

@@ -38,37 +38,9 @@
 #include <type_traits>
 
 #include "attn_params.h"
+#include "lds_tile.h"
 
 namespace trinix {
-
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-
-// Swizzle of the 16-byte units of a D-wide row-major tile row.  K rows are
-// read 16 bytes per lane, 16 consecutive rows per access; V rows are read 8
-// bytes per lane by ds_read_b64_tr_b16, 4 consecutive rows x 64 bytes per
-// 32 lanes.
-template <int D>
-__device__ inline int swz_k(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
-}
-template <int D>
-__device__ inline int swz_v(int row) {
-  return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
-}
-
-// Asynchronous global -> LDS copy (global_load_lds_dwordx4): lane l's 16
-// bytes land at LDS byte address lds_base + 16*l (lds_base wave-uniform).  Issued through asm so that the compiler's wait-count analysis
-// does not see it: an LDS-writing global load makes that analysis wait for
-// all LDS reads in flight (lgkmcnt(0)) at every LDS operand use.  Callers
-// wait for these loads themselves (s_waitcnt vmcnt + barrier) before any
-// wavefront reads the LDS they fill.
-// The global address is a wave-uniform 64-bit base (SGPR pair) plus a
-// per-lane 32-bit byte offset.
-__device__ inline void dma_16b_s(uint32_t offset, uint64_t base, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(offset), "s"(base), "s"(lds_base) : "memory", "m0");
-}
 
 template <class E, int D, int BN, int NW, int OCC, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
@@ -226,14 +198,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     ld_koff[l] = (uint32_t)ld_row(l) * (uint32_t)p.k_ss * 2u + (uint32_t)ld_unit_k(l) * 16u;
     ld_voff[l] = (uint32_t)ld_row(l) * (uint32_t)p.v_ss * 2u + (uint32_t)ld_unit_v(l) * 16u;
   }
-  auto uniform_u64 = [](const void* ptr) __attribute__((always_inline)) -> uint64_t {
-    const uint64_t x = (uint64_t)(uintptr_t)ptr;
-    // readfirstlane returns int: widen through uint32_t (no sign extension)
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)x);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(x >> 32));
-    return (uint64_t)lo | ((uint64_t)hi << 32);
-  };
-  const uint64_t kbase_s = uniform_u64(kbase), vbase_s = uniform_u64(vbase);
+  const uint64_t kbase_s = uniform_ptr(kbase), vbase_s = uniform_ptr(vbase);
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
   auto load_tile = [&](bool is_k, uint64_t base_s, int64_t ss, const uint32_t* offs, uint16_t* lds_tile, int tile)
                        __attribute__((always_inline)) {

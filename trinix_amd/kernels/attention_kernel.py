@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import warnings
 from typing import Optional, Tuple
 
 import torch
@@ -167,137 +168,259 @@ class TritonAttentionKernel:
         return_lse: bool = False,
         use_blockmap: bool = True,
     ):
-        """Attention forward (reference ``attention_kernel.py:497-664``).
+        """Attention forward (reference ``attention_kernel.py:497-664``); the
+        output carries no autograd history, as in the reference.
 
         Extensions (keyword-only): ``rotary_cos``/``rotary_sin`` (rows of the
         reference RoPE tables in ``q.dtype``, indexed by position) apply RoPE
         to q inside the kernel and to k by a pre-pass (``rotary_k=False``
         leaves k as given); ``return_lse`` also returns the (B, H, Sq) fp32
-        log-sum-exp.
+        log-sum-exp.  ``attention()`` is the differentiable entry point.
         """
-        if not (q.is_cuda and k.is_cuda and v.is_cuda):
-            raise ValueError("TritonAttentionKernel requires GPU tensors")
-        if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
-            raise ValueError(f"Expected 4D tensors, got q: {q.shape}, k: {k.shape}, v: {v.shape}")
-        if q.dtype not in _DTYPE_CODE:
-            raise ValueError(f"Unsupported dtype {q.dtype}; use float32, float16 or bfloat16")
-        if k.dtype != q.dtype or v.dtype != q.dtype:
-            raise ValueError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
-        B, Sq, H, D = q.shape
-        Bk, Sk, Hkv, Dk = k.shape
-        if Bk != B or Dk != D or tuple(v.shape) != (B, Sk, Hkv, D):
-            raise ValueError(f"k/v shapes {tuple(k.shape)}, {tuple(v.shape)} don't match q {tuple(q.shape)}")
-        if Hkv <= 0 or H % Hkv != 0:
-            raise ValueError(f"num_heads ({H}) must be a multiple of the KV heads ({Hkv})")
-        d_kernel = kernel_head_dim(D)
-        if d_kernel is None:
-            raise ValueError(f"head_dim {D} > {KERNEL_HEAD_DIMS[-1]} is not supported")
-        if not (0.0 <= dropout_p < 1.0):
-            raise ValueError(f"dropout_p must be in [0, 1), got {dropout_p}")
-        if scale is None:
-            scale = D ** -0.5
-        device = q.device
-        stream = current_stream_ptr(device)
-        lib = nat.load_library()
-
-        if rotary_cos is not None or rotary_sin is not None:
-            if rotary_cos is None or rotary_sin is None:
-                raise ValueError("rotary_cos and rotary_sin must be given together")
-            if D % 2:
-                raise ValueError("RoPE needs an even head_dim")
-            if rotary_cos.shape[0] < max(Sq, Sk) or rotary_cos.shape[-1] < D // 2:
-                raise ValueError("rotary tables are smaller than (seq_len, head_dim/2)")
-            if rotary_k:
-                from .rope_kernel import rope_apply
-                k = rope_apply(k, rotary_cos, rotary_sin)
-            if d_kernel != D:
-                # RoPE pairs (d, d + D/2) of the unpadded head dim: rotate q
-                # here, then pad, rather than fusing at the padded width.
-                from .rope_kernel import rope_apply
-                q = rope_apply(q, rotary_cos, rotary_sin)
-                rotary_cos = rotary_sin = None
-
-        qk = _prepare_operand(q, d_kernel)
-        kk = _prepare_operand(k, d_kernel)
-        vk = _prepare_operand(v, d_kernel)
-        out = torch.empty((B, Sq, H, d_kernel), dtype=q.dtype, device=device)
-
-        args = nat.AttnFwdArgs()
-        args.q, args.k, args.v, args.out = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
-        lse = None
-        if return_lse:
-            lse = torch.empty((B, H, Sq), dtype=torch.float32, device=device)
-            args.lse = lse.data_ptr()
-        args.q_stride = nat.int64x4(qk.stride())
-        args.k_stride = nat.int64x4(kk.stride())
-        args.v_stride = nat.int64x4(vk.stride())
-        args.out_stride = nat.int64x4(out.stride())
-        args.batch, args.seqlen_q, args.seqlen_k = B, Sq, Sk
-        args.nheads_q, args.nheads_kv, args.head_dim = H, Hkv, d_kernel
-        args.dtype = _DTYPE_CODE[q.dtype]
-        args.softmax_scale = float(scale)
-        args.causal = 1 if causal else 0
-        if window_size is not None:
-            wl, wr = window_size
-            args.has_window = 1
-            args.window_left, args.window_right = int(wl), int(wr)
-
-        keep = [qk, kk, vk]  # hold references until the launch returns
-        if alibi_slopes is not None:
-            sl = alibi_slopes
-            if sl.dim() == 1:
-                sl = sl.unsqueeze(0)
-            if sl.dim() != 2 or sl.shape[-1] != H or sl.shape[0] not in (1, B):
-                raise ValueError(f"alibi_slopes shape {tuple(alibi_slopes.shape)} must be (H,), (1, H) or (B, H)")
-            sl = sl.to(device=device, dtype=torch.float32).contiguous()
-            keep.append(sl)
-            args.alibi_slopes = sl.data_ptr()
-            args.alibi_stride = nat.int64x2((H if sl.shape[0] > 1 else 0, 1))
-
-        if attn_mask is not None:
-            m = attn_mask
-            if m.device != device:
-                m = m.to(device)
-            if m.dtype == torch.bool:
-                m = m.view(torch.uint8)
-            elif m.dtype not in _MASK_DTYPE_CODE:
-                m = m.to(torch.float32)
-            m4 = TritonAttentionKernel._prepare_mask(m, B, H, Sq, Sk)
-            keep.append(m4)
-            args.mask = m4.data_ptr()
-            args.mask_dtype = _MASK_DTYPE_CODE[m4.dtype]
-            args.mask_stride = nat.int64x4(m4.stride())
-            if use_blockmap:
-                bmap, bst = TritonAttentionKernel.mask_blockmap(m4, stream)
-                keep.append(bmap)
-                args.mask_blockmap = bmap.data_ptr()
-                args.blockmap_stride = nat.int64x2(bst)
-
-        if dropout_p > 0.0:
-            # Seed from torch's CPU generator: no device->host sync.
-            args.dropout_p = float(dropout_p)
-            args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
-            args.dropout_offset = 0
-
-        if rotary_cos is not None:
-            cos = rotary_cos.to(device=device, dtype=q.dtype)
-            sin = rotary_sin.to(device=device, dtype=q.dtype)
-            if cos.stride(-1) != 1 or cos.stride(0) % 8 or cos.data_ptr() % 16:
-                cos = cos.contiguous()
-            if sin.stride(-1) != 1 or sin.stride(0) != cos.stride(0) or sin.data_ptr() % 16:
-                sin = sin.contiguous()
-                if sin.stride(0) != cos.stride(0):
-                    cos = cos.contiguous()
-            keep += [cos, sin]
-            args.rope_cos, args.rope_sin, args.rope_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
-
-        rc = lib.trinix_attn_fwd(ctypes.byref(args), stream)
-        nat.check(rc, "trinix_attn_fwd")
-        if d_kernel != D:
-            out = out[..., :D].contiguous()
+        out, lse, _ = _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes,
+                               rotary_cos, rotary_sin, rotary_k, return_lse, use_blockmap)
         if return_lse:
             return out, lse
         return out
+
+
+def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, rotary_cos, rotary_sin,
+             rotary_k, return_lse, use_blockmap, keep_state=False):
+    """Launch ``trinix_attn_fwd``; returns (out, lse or None, state).  With
+    ``keep_state`` the prepared operands (padded, strided as the kernel reads
+    them), the lse and the mask / slope tensors are kept for the backward."""
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("TritonAttentionKernel requires GPU tensors")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError(f"Expected 4D tensors, got q: {q.shape}, k: {k.shape}, v: {v.shape}")
+    if q.dtype not in _DTYPE_CODE:
+        raise ValueError(f"Unsupported dtype {q.dtype}; use float32, float16 or bfloat16")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
+    B, Sq, H, D = q.shape
+    Bk, Sk, Hkv, Dk = k.shape
+    if Bk != B or Dk != D or tuple(v.shape) != (B, Sk, Hkv, D):
+        raise ValueError(f"k/v shapes {tuple(k.shape)}, {tuple(v.shape)} don't match q {tuple(q.shape)}")
+    if Hkv <= 0 or H % Hkv != 0:
+        raise ValueError(f"num_heads ({H}) must be a multiple of the KV heads ({Hkv})")
+    d_kernel = kernel_head_dim(D)
+    if d_kernel is None:
+        raise ValueError(f"head_dim {D} > {KERNEL_HEAD_DIMS[-1]} is not supported")
+    if not (0.0 <= dropout_p < 1.0):
+        raise ValueError(f"dropout_p must be in [0, 1), got {dropout_p}")
+    if scale is None:
+        scale = D ** -0.5
+    device = q.device
+    stream = current_stream_ptr(device)
+    lib = nat.load_library()
+
+    if rotary_cos is not None or rotary_sin is not None:
+        if rotary_cos is None or rotary_sin is None:
+            raise ValueError("rotary_cos and rotary_sin must be given together")
+        if D % 2:
+            raise ValueError("RoPE needs an even head_dim")
+        if rotary_cos.shape[0] < max(Sq, Sk) or rotary_cos.shape[-1] < D // 2:
+            raise ValueError("rotary tables are smaller than (seq_len, head_dim/2)")
+        if rotary_k:
+            from .rope_kernel import rope_apply
+            k = rope_apply(k, rotary_cos, rotary_sin)
+        if d_kernel != D:
+            # RoPE pairs (d, d + D/2) of the unpadded head dim: rotate q
+            # here, then pad, rather than fusing at the padded width.
+            from .rope_kernel import rope_apply
+            q = rope_apply(q, rotary_cos, rotary_sin)
+            rotary_cos = rotary_sin = None
+
+    qk = _prepare_operand(q, d_kernel)
+    kk = _prepare_operand(k, d_kernel)
+    vk = _prepare_operand(v, d_kernel)
+    out = torch.empty((B, Sq, H, d_kernel), dtype=q.dtype, device=device)
+
+    args = nat.AttnFwdArgs()
+    args.q, args.k, args.v, args.out = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr()
+    lse = None
+    if return_lse or keep_state:
+        lse = torch.empty((B, H, Sq), dtype=torch.float32, device=device)
+        args.lse = lse.data_ptr()
+    args.q_stride = nat.int64x4(qk.stride())
+    args.k_stride = nat.int64x4(kk.stride())
+    args.v_stride = nat.int64x4(vk.stride())
+    args.out_stride = nat.int64x4(out.stride())
+    args.batch, args.seqlen_q, args.seqlen_k = B, Sq, Sk
+    args.nheads_q, args.nheads_kv, args.head_dim = H, Hkv, d_kernel
+    args.dtype = _DTYPE_CODE[q.dtype]
+    args.softmax_scale = float(scale)
+    args.causal = 1 if causal else 0
+    if window_size is not None:
+        wl, wr = window_size
+        args.has_window = 1
+        args.window_left, args.window_right = int(wl), int(wr)
+
+    keep = [qk, kk, vk]  # hold references until the launch returns
+    if alibi_slopes is not None:
+        sl = alibi_slopes
+        if sl.dim() == 1:
+            sl = sl.unsqueeze(0)
+        if sl.dim() != 2 or sl.shape[-1] != H or sl.shape[0] not in (1, B):
+            raise ValueError(f"alibi_slopes shape {tuple(alibi_slopes.shape)} must be (H,), (1, H) or (B, H)")
+        sl = sl.to(device=device, dtype=torch.float32).contiguous()
+        keep.append(sl)
+        args.alibi_slopes = sl.data_ptr()
+        args.alibi_stride = nat.int64x2((H if sl.shape[0] > 1 else 0, 1))
+
+    if attn_mask is not None:
+        m = attn_mask
+        if m.device != device:
+            m = m.to(device)
+        if m.dtype == torch.bool:
+            m = m.view(torch.uint8)
+        elif m.dtype not in _MASK_DTYPE_CODE:
+            m = m.to(torch.float32)
+        m4 = TritonAttentionKernel._prepare_mask(m, B, H, Sq, Sk)
+        keep.append(m4)
+        args.mask = m4.data_ptr()
+        args.mask_dtype = _MASK_DTYPE_CODE[m4.dtype]
+        args.mask_stride = nat.int64x4(m4.stride())
+        if use_blockmap:
+            bmap, bst = TritonAttentionKernel.mask_blockmap(m4, stream)
+            keep.append(bmap)
+            args.mask_blockmap = bmap.data_ptr()
+            args.blockmap_stride = nat.int64x2(bst)
+
+    if dropout_p > 0.0:
+        # Seed from torch's CPU generator: no device->host sync.
+        args.dropout_p = float(dropout_p)
+        args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+        args.dropout_offset = 0
+
+    if rotary_cos is not None:
+        cos = rotary_cos.to(device=device, dtype=q.dtype)
+        sin = rotary_sin.to(device=device, dtype=q.dtype)
+        if cos.stride(-1) != 1 or cos.stride(0) % 8 or cos.data_ptr() % 16:
+            cos = cos.contiguous()
+        if sin.stride(-1) != 1 or sin.stride(0) != cos.stride(0) or sin.data_ptr() % 16:
+            sin = sin.contiguous()
+            if sin.stride(0) != cos.stride(0):
+                cos = cos.contiguous()
+        keep += [cos, sin]
+        args.rope_cos, args.rope_sin, args.rope_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+
+    rc = lib.trinix_attn_fwd(ctypes.byref(args), stream)
+    nat.check(rc, "trinix_attn_fwd")
+    state = None
+    if keep_state:
+        state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),
+                     window=window_size, D=D, d_kernel=d_kernel, keep=keep, args=args)
+    if d_kernel != D:
+        out = out[..., :D].contiguous()
+    return out, lse, state
+
+
+def _backward(state, dout):
+    """Launch ``trinix_attn_bwd`` for a forward run with ``keep_state``;
+    returns (dq, dk, dv) at the caller's head_dim, in the input dtype."""
+    qk, kk, vk, out, lse = state["q"], state["k"], state["v"], state["out"], state["lse"]
+    fa = state["args"]
+    D, dkrn = state["D"], state["d_kernel"]
+    B, Sq, H, _ = qk.shape
+    Sk, Hkv = kk.shape[1], kk.shape[2]
+    do = _prepare_operand(dout.to(qk.dtype), dkrn)
+    dq = torch.empty((B, Sq, H, dkrn), dtype=qk.dtype, device=qk.device)
+    dk = torch.empty((B, Sk, Hkv, dkrn), dtype=qk.dtype, device=qk.device)
+    dv = torch.empty((B, Sk, Hkv, dkrn), dtype=qk.dtype, device=qk.device)
+    delta = torch.empty((B, H, Sq), dtype=torch.float32, device=qk.device)
+    a = nat.AttnBwdArgs()
+    a.q, a.k, a.v, a.out, a.dout = qk.data_ptr(), kk.data_ptr(), vk.data_ptr(), out.data_ptr(), do.data_ptr()
+    a.lse, a.delta = lse.data_ptr(), delta.data_ptr()
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    for name, t in (("q", qk), ("k", kk), ("v", vk), ("out", out), ("dout", do), ("dq", dq), ("dk", dk),
+                    ("dv", dv)):
+        setattr(a, name + "_stride", nat.int64x4(t.stride()))
+    a.batch, a.seqlen_q, a.seqlen_k, a.nheads_q, a.nheads_kv, a.head_dim = B, Sq, Sk, H, Hkv, dkrn
+    a.dtype = _DTYPE_CODE[qk.dtype]
+    a.softmax_scale = fa.softmax_scale
+    a.causal, a.has_window = fa.causal, fa.has_window
+    a.window_left, a.window_right = fa.window_left, fa.window_right
+    a.alibi_slopes, a.alibi_stride = fa.alibi_slopes, fa.alibi_stride
+    a.mask, a.mask_dtype, a.mask_stride = fa.mask, fa.mask_dtype, fa.mask_stride
+    a.mask_blockmap, a.blockmap_stride = fa.mask_blockmap, fa.blockmap_stride
+    rc = nat.load_library().trinix_attn_bwd(ctypes.byref(a), current_stream_ptr(qk.device))
+    nat.check(rc, "trinix_attn_bwd")
+    if dkrn != D:
+        dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
+    return dq, dk, dv
+
+
+class _HipAttnFunction(torch.autograd.Function):
+    """Differentiable attention: ``trinix_attn_fwd`` forward (keeping the
+    log-sum-exp) and ``trinix_attn_bwd`` backward.  RoPE of q (and of k when
+    ``rotary_k``) is applied here before the forward, and the gradients are
+    rotated back (the RoPE kernel with -sin) in the backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, attn_mask, causal, scale, window_size, alibi_slopes, rotary_cos, rotary_sin, rotary_k,
+                return_lse):
+        from .rope_kernel import rope_apply
+
+        ctx.rope = None
+        if rotary_cos is not None:
+            q = rope_apply(q, rotary_cos, rotary_sin)
+            if rotary_k:
+                k = rope_apply(k, rotary_cos, rotary_sin)
+            ctx.rope = (rotary_cos, rotary_sin, rotary_k)
+        out, lse, state = _forward(q, k, v, attn_mask, causal, scale, 0.0, window_size, alibi_slopes, None, None,
+                                   True, True, True, keep_state=True)
+        ctx.state = state
+        if return_lse:
+            ctx.mark_non_differentiable(lse)
+            return out, lse
+        return out
+
+    @staticmethod
+    def backward(ctx, dout, *unused):
+        dq, dk, dv = _backward(ctx.state, dout.contiguous())
+        ctx.state = None
+        if ctx.rope is not None:
+            from .rope_kernel import rope_apply
+
+            cos, sin, rot_k = ctx.rope
+            neg = -sin
+            dq = rope_apply(dq, cos, neg)
+            if rot_k:
+                dk = rope_apply(dk, cos, neg)
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None
+
+
+_warned_no_grad = set()
+
+
+def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, window_size=None, alibi_slopes=None,
+              *, rotary_cos=None, rotary_sin=None, rotary_k=True, return_lse=False):
+    """Attention with gradients when q, k or v require them (bf16/fp16, no
+    dropout); otherwise, and in those cases, ``TritonAttentionKernel.apply``.
+
+    The reference's Triton attention has no backward (its output is detached,
+    ``attention_kernel.py:497-517``).  Here bf16/fp16 attention without
+    dropout is differentiable through ``trinix_attn_bwd``.  fp32 or dropout
+    with gradients required keep the reference's behaviour, a detached
+    output, and warn once.
+    """
+    needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+    if needs_grad:
+        if q.dtype in (torch.float16, torch.bfloat16) and dropout_p == 0.0:
+            if scale is None:
+                scale = q.shape[-1] ** -0.5
+            return _HipAttnFunction.apply(q, k, v, attn_mask, causal, scale, window_size, alibi_slopes, rotary_cos,
+                                          rotary_sin, rotary_k, return_lse)
+        key = (q.dtype, dropout_p > 0.0)
+        if key not in _warned_no_grad:
+            _warned_no_grad.add(key)
+            warnings.warn("HIP attention backward runs in bf16/fp16 without dropout; this call's output is "
+                          "detached (no gradient flows through it), as in the reference Triton path",
+                          stacklevel=2)
+    return TritonAttentionKernel.apply(q, k, v, attn_mask=attn_mask, causal=causal, scale=scale, dropout_p=dropout_p,
+                                       window_size=window_size, alibi_slopes=alibi_slopes, rotary_cos=rotary_cos,
+                                       rotary_sin=rotary_sin, rotary_k=rotary_k, return_lse=return_lse)
 
 
 def attention_flops(batch: int, nheads: int, seqlen_q: int, seqlen_k: int, head_dim: int,

@@ -71,6 +71,30 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     return out
 
 
+class _RoPEFunction(torch.autograd.Function):
+    """RoPE of one tensor; the backward is the rotation by -theta."""
+
+    @staticmethod
+    def forward(ctx, x, cos, sin, position_ids):
+        ctx.save_for_backward(cos, sin)
+        ctx.position_ids = position_ids
+        return rope_apply(x, cos, sin, position_ids)
+
+    @staticmethod
+    def backward(ctx, grad):
+        cos, sin = ctx.saved_tensors
+        return rope_apply(grad, cos, -sin, ctx.position_ids), None, None, None
+
+
+def rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+           position_ids: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``rope_apply`` that records the inverse rotation for autograd when x
+    requires a gradient."""
+    if torch.is_grad_enabled() and x.requires_grad:
+        return _RoPEFunction.apply(x, cos, sin, position_ids)
+    return rope_apply(x, cos, sin, position_ids)
+
+
 class TritonRoPEKernel:
     """RoPE on q and k (name kept from the reference for drop-in use)."""
 

@@ -29,7 +29,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ...kernels.attention_kernel import TritonAttentionKernel
+from ...kernels.attention_kernel import TritonAttentionKernel, attention
 
 
 class _QKRMSNorm(nn.Module):
@@ -271,7 +271,7 @@ class FastBaseAttention(nn.Module):
         kw = {}
         if rotary is not None:
             kw = dict(rotary_cos=rotary[0], rotary_sin=rotary[1], rotary_k=False)
-        return TritonAttentionKernel.apply(
+        return attention(
             q, k, v, attn_mask=attn_mask, causal=self.causal, scale=self.scale,
             dropout_p=self.dropout if self.training else 0.0, window_size=self._window_size(),
             alibi_slopes=self._alibi_slopes(), **kw)
@@ -300,9 +300,9 @@ class FastBaseAttention(nn.Module):
             # q is rotated inside the attention kernel; k by the RoPE kernel
             # (it is also the returned cache).
             cos, sin = self.position_embedding(q, max(seq_len_q, seq_len_k))
-            from ...kernels.rope_kernel import rope_apply
+            from ...kernels.rope_kernel import rotate
 
-            k = rope_apply(k, cos, sin)
+            k = rotate(k, cos, sin)
             rotary = (cos, sin)
         else:
             q, k, position_bias = self._apply_position_embedding(q, k, seq_len_q, seq_len_k, bs, position_ids)

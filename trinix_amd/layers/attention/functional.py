@@ -6,7 +6,7 @@ from typing import Optional, Tuple
 
 import torch
 
-from ...kernels.attention_kernel import TritonAttentionKernel
+from ...kernels.attention_kernel import TritonAttentionKernel, attention
 
 
 def triton_attn_func(
@@ -45,7 +45,9 @@ def triton_attn_func(
         return_lse: also return the fp32 (B, H, Sq) log-sum-exp.
 
     Returns:
-        (batch, seq_len_q, num_heads, head_dim) tensor of q.dtype.
+        (batch, seq_len_q, num_heads, head_dim) tensor of q.dtype.  For
+        bf16/fp16 inputs without dropout it is differentiable (HIP backward;
+        the reference's output is detached).
 
     Raises:
         ValueError: non-GPU tensors or inconsistent shapes.
@@ -78,7 +80,7 @@ def triton_attn_func(
     if softmax_scale is None:
         softmax_scale = headdim**-0.5
 
-    return TritonAttentionKernel.apply(
+    return attention(
         q,
         k,
         v,

@@ -12,7 +12,7 @@ from typing import Optional, Tuple
 import torch
 import torch.nn as nn
 
-from ...kernels.rope_kernel import rope_apply
+from ...kernels.rope_kernel import rotate
 
 
 class FastRoPEPositionEmbedding(nn.Module):
@@ -51,7 +51,7 @@ class FastRoPEPositionEmbedding(nn.Module):
     def apply_rotary_pos_emb(self, q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                              position_ids: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         if q.is_cuda:
-            return rope_apply(q, cos, sin, position_ids), rope_apply(k, cos, sin, position_ids)
+            return rotate(q, cos, sin, position_ids), rotate(k, cos, sin, position_ids)
         if position_ids is not None:
             c = cos[position_ids].unsqueeze(2)
             s = sin[position_ids].unsqueeze(2)
