@@ -135,6 +135,30 @@ def cold_step_ms(fn, torch, iters=10):
     return sorted(times)[len(times) // 2]
 
 
+def fwd_bwd_ms(w, inp, torch, iters=10):
+    """ms of one differentiable step on the workload: forward (with the
+    workload's RoPE) and backward to q, k, v through the HIP kernels."""
+    from trinix_amd import triton_attn_func
+
+    q, k, v = (t.detach().clone().requires_grad_(True) for t in (inp.q, inp.k, inp.v))
+    do = torch.randn_like(inp.q)
+    kw = dict(causal=w.causal, window_size=w.window)
+    if inp.cos is not None:
+        kw.update(rotary_cos=inp.cos, rotary_sin=inp.sin)
+
+    def step():
+        triton_attn_func(q, k, v, **kw).backward(do)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / iters
+
+
 def measure(w, args, torch, cold=False):
     from trinix_amd.workloads import make_inputs, flops
 
@@ -272,6 +296,11 @@ def main():
         # the same step with q/k/v evicted from the 256 MB MALL before each call
         "cold_mall": {"ms_per_step": round(cold_ms, 4), "tflops": round(fl / cold_ms / 1e9, 2)},
     }
+    if dname in ("bf16", "fp16") and not w.alibi and not w.block_mask:
+        # forward + backward (3.5x the forward FLOP by the usual convention)
+        fb = fwd_bwd_ms(w, inp, torch)
+        rec["fwd_bwd"] = {"ms": round(fb, 4), "tflops": round(3.5 * fl / fb / 1e9, 2),
+                          "bwd_ms": round(fb - ms, 4), "bwd_tflops": round(2.5 * fl / (fb - ms) / 1e9, 2)}
     if args.all:
         extra = {}
         for name, wo in WORKLOADS.items():
