@@ -17,6 +17,11 @@
  *                                 trinix/kernels/attention_kernel.py:497-664
  *                                 (launch of _fwd_kernel :234-434 and
  *                                 _fwd_kernel_with_mask :8-231)
+ *   trinix_attn_fwd_splitkv,   <- TritonAttentionKernel.apply for seqlen_q != seqlen_k
+ *   trinix_attn_fwd_splitkv_plan  (asserted away at attention_kernel.py:510; the
+ *                                 layers' KV-cache decode, e.g.
+ *                                 grouped_query_attention.py:179-187, runs the
+ *                                 eager path base.py:347-400)
  *   trinix_attn_mask_blockmap  <- TritonAttentionKernel._prepare_mask
  *                                 trinix/kernels/attention_kernel.py:479-495
  *                                 (the (B,H,S,S) materialisation is replaced
@@ -112,6 +117,30 @@ typedef struct trinix_attn_fwd_args {
 
 /* Attention forward on `stream`. */
 int trinix_attn_fwd(const trinix_attn_fwd_args* args, void* stream);
+
+/* Split-KV forward for decode-shaped calls (seqlen_q <= 16 against a long
+ * KV cache), same semantics and arguments as trinix_attn_fwd.  Extension:
+ * the reference asserts seqlen_q == seqlen_k (attention_kernel.py:510) and
+ * its layers' cache path runs the eager attention (base.py:347-400).
+ * The rows of one KV head's q-heads are packed into 16-row tiles, and the
+ * keys any row may see are cut into `num_splits` chunks merged by their
+ * log-sum-exp.
+ *
+ * trinix_attn_fwd_splitkv_plan: *num_splits = 0 if the split-KV kernel does
+ * not apply (fp32, dropout, fused RoPE, seqlen_q > 16, no visible key): use
+ * trinix_attn_fwd.  Otherwise the chunk count and the size of the fp32
+ * workspace trinix_attn_fwd_splitkv needs (0 for a single chunk).  Host
+ * only, no launch.
+ * trinix_attn_fwd_splitkv: the forward on `stream`; `workspace` is
+ * caller-owned device memory of at least the planned size, 16-byte aligned
+ * (may be NULL when the plan asks for 0 bytes).  Returns
+ * TRINIX_ERR_BAD_ARGUMENT where the plan does not apply or the workspace is
+ * too small. */
+int trinix_attn_fwd_splitkv_plan(const trinix_attn_fwd_args* args,
+                                 int32_t* num_splits,
+                                 int64_t* workspace_bytes);
+int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* args, void* workspace,
+                            int64_t workspace_bytes, void* stream);
 
 /* Block classification of an additive mask of logical size
  * (mb, mh, seqlen_q, seqlen_k) with element strides `stride` (0 = broadcast).

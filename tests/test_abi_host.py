@@ -136,3 +136,50 @@ def test_kernel_head_dim_padding_rule():
     from trinix_amd.kernels.attention_kernel import kernel_head_dim
 
     assert [kernel_head_dim(d) for d in (8, 32, 64, 65, 80, 128, 129)] == [64, 64, 64, 128, 128, 128, None]
+
+
+def _plan(lib, **kw):
+    a = _args(**kw)
+    ns, wb = ctypes.c_int32(-1), ctypes.c_int64(-1)
+    assert lib.trinix_attn_fwd_splitkv_plan(ctypes.byref(a), ctypes.byref(ns), ctypes.byref(wb)) == nat.TRINIX_OK
+    return ns.value, wb.value
+
+
+def test_splitkv_plan(lib):
+    """Host-only split plan of the decode kernel: rows of a KV head's q-heads
+    packed 16 to a tile, the visible keys cut into chunks of >= 128 keys
+    (multiples of 64) until about 1024 workgroups exist; fp32 partial O and
+    lse per (row, chunk) when there is more than one chunk."""
+    dec = dict(seqlen_q=1, seqlen_k=8192, nheads_q=32, nheads_kv=8)
+    # 8 (batch, KV head) items -> 128 chunks wanted, capped at 8192/128 = 64
+    assert _plan(lib, **dec) == (64, 8 * 4 * 64 * (128 + 1) * 4)
+    # batch 8: 64 items -> 16 chunks of 512 keys; batch 64: 512 items -> 2 chunks
+    assert _plan(lib, **dec, batch=8) == (16, 8 * 8 * 4 * 16 * 129 * 4)
+    assert _plan(lib, **dec, batch=64) == (2, 64 * 8 * 4 * 2 * 129 * 4)
+    # >= 1024 items: one chunk, the output is written directly (no workspace)
+    assert _plan(lib, **dec, batch=128) == (1, 0)
+    # 3 rows x G=4 = 12 packed rows, D=64, 1000 keys -> ceil(1000/128)=8 chunks of 128
+    assert _plan(lib, seqlen_q=3, seqlen_k=1000, nheads_q=8, nheads_kv=2, head_dim=64) == (8, 2 * 12 * 8 * 65 * 4)
+    # top-left causal with one query row sees key 0 only; a window bounds the span
+    assert _plan(lib, **dec, causal=1) == (1, 0)
+    assert _plan(lib, **dec, has_window=1, window_left=10, window_right=300) == (3, 8 * 4 * 3 * 129 * 4)
+    # not applicable -> 0 chunks (trinix_attn_fwd is the path)
+    assert _plan(lib, **dec, dtype=nat.TRINIX_F32)[0] == 0
+    assert _plan(lib, **dec, dropout_p=0.1)[0] == 0
+    assert _plan(lib, **dict(dec, seqlen_q=17))[0] == 0
+    assert _plan(lib, **dec, rope_cos=4096, rope_sin=4096, rope_stride=64)[0] == 0
+    assert _plan(lib, **dec, has_window=1, window_left=-10, window_right=-20)[0] == 0  # no visible key
+
+
+def test_splitkv_rejects_before_launch(lib):
+    a = _args(seqlen_q=1, seqlen_k=8192, nheads_q=32, nheads_kv=8)
+    _, need = _plan(lib, seqlen_q=1, seqlen_k=8192, nheads_q=32, nheads_kv=8)
+    assert lib.trinix_attn_fwd_splitkv(ctypes.byref(a), 4096, need - 4, None) == nat.TRINIX_ERR_BAD_ARGUMENT
+    assert lib.trinix_attn_fwd_splitkv(ctypes.byref(a), None, need, None) == nat.TRINIX_ERR_BAD_ARGUMENT
+    assert lib.trinix_attn_fwd_splitkv(ctypes.byref(a), 4100, need, None) == nat.TRINIX_ERR_BAD_ARGUMENT
+    f32 = _args(seqlen_q=1, seqlen_k=8192, dtype=nat.TRINIX_F32)
+    assert lib.trinix_attn_fwd_splitkv(ctypes.byref(f32), 4096, 1 << 30, None) == nat.TRINIX_ERR_BAD_ARGUMENT
+    ns, wb = ctypes.c_int32(), ctypes.c_int64()
+    assert lib.trinix_attn_fwd_splitkv_plan(ctypes.byref(_args(head_dim=96)), ctypes.byref(ns),
+                                            ctypes.byref(wb)) == nat.TRINIX_ERR_BAD_HEAD_DIM
+    assert lib.trinix_attn_fwd_splitkv_plan(ctypes.byref(a), None, ctypes.byref(wb)) == nat.TRINIX_ERR_NULL_POINTER

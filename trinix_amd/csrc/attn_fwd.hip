@@ -292,6 +292,43 @@ Cfg16 pick_cfg16(int64_t batch, int64_t hq, int64_t sq) {
 
 }  // namespace
 
+namespace trinix {
+
+int validate_fwd_args(const trinix_attn_fwd_args* a) {
+  if (!a) return TRINIX_ERR_NULL_POINTER;
+  const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
+  if (a->dtype != TRINIX_F32 && a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0)
+    return TRINIX_ERR_BAD_SHAPE;
+  if (a->nheads_q % a->nheads_kv != 0) return TRINIX_ERR_BAD_SHAPE;
+  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
+    return TRINIX_ERR_BAD_SHAPE;
+  int rc;
+  if ((rc = check_tensor(a->q, a->q_stride, esize))) return rc;
+  if ((rc = check_tensor(a->k, a->k_stride, esize))) return rc;
+  if ((rc = check_tensor(a->v, a->v_stride, esize))) return rc;
+  // 16-bit kernels address a K/V tile (up to 128 key rows) as one base plus
+  // per-lane 32-bit byte offsets: the key-row stride must be in [0, 2^22).
+  if (esize == 2 && (a->k_stride[1] < 0 || a->k_stride[1] >= kMaxKvRowStride || a->v_stride[1] < 0 ||
+                     a->v_stride[1] >= kMaxKvRowStride))
+    return TRINIX_ERR_BAD_STRIDE;
+  if ((rc = check_tensor(a->out, a->out_stride, esize))) return rc;
+  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
+      a->mask_dtype != TRINIX_U8)
+    return TRINIX_ERR_BAD_DTYPE;
+  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
+  if (a->rope_cos && esize == 2 &&
+      (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
+    return TRINIX_ERR_BAD_STRIDE;
+
+  return TRINIX_OK;
+}
+
+}  // namespace trinix
+
 extern "C" {
 
 int trinix_abi_version(void) { return TRINIX_ATTN_ABI_VERSION; }
@@ -344,34 +381,8 @@ int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* ou
 }
 
 int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
-  if (!a) return TRINIX_ERR_NULL_POINTER;
-  const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
-  if (a->dtype != TRINIX_F32 && a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
-  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0)
-    return TRINIX_ERR_BAD_SHAPE;
-  if (a->nheads_q % a->nheads_kv != 0) return TRINIX_ERR_BAD_SHAPE;
-  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
-    return TRINIX_ERR_BAD_SHAPE;
-  int rc;
-  if ((rc = check_tensor(a->q, a->q_stride, esize))) return rc;
-  if ((rc = check_tensor(a->k, a->k_stride, esize))) return rc;
-  if ((rc = check_tensor(a->v, a->v_stride, esize))) return rc;
-  // 16-bit kernels address a K/V tile (up to 128 key rows) as one base plus
-  // per-lane 32-bit byte offsets: the key-row stride must be in [0, 2^22).
-  if (esize == 2 && (a->k_stride[1] < 0 || a->k_stride[1] >= kMaxKvRowStride || a->v_stride[1] < 0 ||
-                     a->v_stride[1] >= kMaxKvRowStride))
-    return TRINIX_ERR_BAD_STRIDE;
-  if ((rc = check_tensor(a->out, a->out_stride, esize))) return rc;
-  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
-      a->mask_dtype != TRINIX_U8)
-    return TRINIX_ERR_BAD_DTYPE;
-  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
-  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
-  if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
-  if (a->rope_cos && esize == 2 &&
-      (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
-    return TRINIX_ERR_BAD_STRIDE;
+  const int vrc = validate_fwd_args(a);
+  if (vrc != TRINIX_OK) return vrc;
 
   FwdParams p;
   p.q = (const uint16_t*)a->q;

@@ -84,6 +84,10 @@ hipError_t launch_attn16_bf16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipS
 hipError_t launch_attn16_f16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 hipError_t launch_attn16_f16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 
+// Host-side argument checks of trinix_attn_fwd (no launch); also applied by
+// the split-KV entry points.
+int validate_fwd_args(const trinix_attn_fwd_args* a);
+
 // Feature bits of a launch (compile-time flags of the 16-bit kernels).
 enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4 };
 

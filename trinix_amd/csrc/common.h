@@ -25,7 +25,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 // v_cvt_pk_f16_f32).  mfma() is D = A*B + C for a 32x32x16 tile: lane l
 // supplies row (l%32) of A and column (l%32) of B, 8 consecutive k each for
 // k-group l/32; D element v of lane l is row (v/4)*8 + (l/32)*4 + v%4,
-// column l%32.
+// column l%32.  mfma16() is the 16x16x32 tile: lane l supplies row (l%16)
+// of A and column (l%16) of B, 8 consecutive k each for k-group l/16; D
+// element v of lane l is row (l/16)*4 + v, column l%16.
 struct BF16 {
   __device__ static inline float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ static inline float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -39,6 +41,10 @@ struct BF16 {
   }
   __device__ static inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
   }
 };
@@ -55,6 +61,10 @@ struct F16 {
   }
   __device__ static inline f32x16_t mfma(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static inline f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
                                                   __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
   }
 };

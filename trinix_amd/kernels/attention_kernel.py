@@ -45,6 +45,13 @@ _MASK_DTYPE_CODE = {
 KERNEL_HEAD_DIMS = (64, 128)
 
 
+# Calls with at most this many query rows (bf16/fp16, no dropout) go to the
+# split-KV decode kernel when its plan applies; SPLITKV_ENABLED = False
+# forces the prefill kernel (tests compare the two).
+SPLITKV_MAX_SQ = 16
+SPLITKV_ENABLED = True
+
+
 def kernel_head_dim(head_dim: int) -> Optional[int]:
     """Head dim the kernels run at: inputs are zero-padded up to it."""
     for d in KERNEL_HEAD_DIMS:
@@ -231,6 +238,14 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             q = rope_apply(q, rotary_cos, rotary_sin)
             rotary_cos = rotary_sin = None
 
+    # Decode-shaped calls (few query rows, long KV) take the split-KV kernel;
+    # it has no fused RoPE, so q is rotated here first.
+    split_kv = SPLITKV_ENABLED and Sq <= SPLITKV_MAX_SQ and q.dtype != torch.float32 and dropout_p == 0.0
+    if split_kv and rotary_cos is not None:
+        from .rope_kernel import rope_apply
+        q = rope_apply(q, rotary_cos, rotary_sin)
+        rotary_cos = rotary_sin = None
+
     qk = _prepare_operand(q, d_kernel)
     kk = _prepare_operand(k, d_kernel)
     vk = _prepare_operand(v, d_kernel)
@@ -281,7 +296,7 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
         args.mask = m4.data_ptr()
         args.mask_dtype = _MASK_DTYPE_CODE[m4.dtype]
         args.mask_stride = nat.int64x4(m4.stride())
-        if use_blockmap:
+        if use_blockmap and not split_kv:
             bmap, bst = TritonAttentionKernel.mask_blockmap(m4, stream)
             keep.append(bmap)
             args.mask_blockmap = bmap.data_ptr()
@@ -305,8 +320,20 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
         keep += [cos, sin]
         args.rope_cos, args.rope_sin, args.rope_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
 
-    rc = lib.trinix_attn_fwd(ctypes.byref(args), stream)
-    nat.check(rc, "trinix_attn_fwd")
+    launched = False
+    if split_kv:
+        ns, wsb = ctypes.c_int32(0), ctypes.c_int64(0)
+        rc = lib.trinix_attn_fwd_splitkv_plan(ctypes.byref(args), ctypes.byref(ns), ctypes.byref(wsb))
+        nat.check(rc, "trinix_attn_fwd_splitkv_plan")
+        if ns.value > 0:
+            ws = torch.empty(wsb.value, dtype=torch.uint8, device=device) if wsb.value else None
+            rc = lib.trinix_attn_fwd_splitkv(ctypes.byref(args), None if ws is None else ws.data_ptr(), wsb.value,
+                                             stream)
+            nat.check(rc, "trinix_attn_fwd_splitkv")
+            launched = True
+    if not launched:
+        rc = lib.trinix_attn_fwd(ctypes.byref(args), stream)
+        nat.check(rc, "trinix_attn_fwd")
     state = None
     if keep_state:
         state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),

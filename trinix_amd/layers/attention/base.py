@@ -242,7 +242,9 @@ class FastBaseAttention(nn.Module):
         qh = q.transpose(1, 2).contiguous().view(batch_size * num_heads, seq_len, head_dim)
         kh = k.transpose(1, 2).contiguous().view(batch_size * num_heads, seq_len_k, head_dim)
         vh = v.transpose(1, 2).contiguous().view(batch_size * num_heads, seq_len_k, head_dim)
-        w = torch.bmm(qh, kh.transpose(-2, -1)) * self.scale
+        # k^T materialised: bf16 bmm with a transposed-view right operand is
+        # avoided on ROCm (it has faulted the GPU); the products are the same.
+        w = torch.bmm(qh, kh.transpose(-2, -1).contiguous()) * self.scale
         if self.causal:
             w.masked_fill_(torch.triu(torch.ones(seq_len, seq_len_k, device=q.device), diagonal=1).bool(),
                            float("-inf"))
