@@ -27,6 +27,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "attn fwd TFLOP/s + % of MI355X bf16 MFMA peak (1 GPU); vs CPU ref ms"
 PEAK_TFLOPS = {"bf16": 2516.6, "fp16": 2516.6, "fp32": 157.3}
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
 DTYPE_NAME = {"torch.bfloat16": "bf16", "torch.float16": "fp16", "torch.float32": "fp32"}
 
 
@@ -188,6 +189,53 @@ def measure(w, args, torch, cold=False):
     return inp, fl, ms, kms, cold_ms
 
 
+DECODE = dict(batch=16, seqlen_k=8192, nheads_q=32, nheads_kv=8, head_dim=128)
+
+
+def decode_measure(torch, iters=30):
+    """One decode step of the C3 model (Llama-3-8B GQA, bf16) against a KV
+    cache: B=16 sequences, 1 query row each, 8192 cached keys.  The split-KV
+    kernel and its merge are HBM-bound: the algorithmic bytes are the K and V
+    caches read once (q and out are 0.1% of it).  Timed with HIP events on
+    the launch stream over back-to-back calls (the GPU, not the host, is the
+    bottleneck at this size)."""
+    import ctypes
+    from trinix_amd import triton_attn_func
+    from trinix_amd import _native as nat
+
+    c = DECODE
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(c["batch"], 1, c["nheads_q"], c["head_dim"], device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(c["batch"], c["seqlen_k"], c["nheads_kv"], c["head_dim"], device="cuda",
+                    generator=g).to(torch.bfloat16)
+    v = torch.randn_like(k)
+    for _ in range(5):
+        triton_attn_func(q, k, v)
+    us = time_events(lambda: triton_attn_func(q, k, v), iters, torch) * 1e3
+    kv_bytes = 2 * k.numel() * k.element_size()
+    a = nat.AttnFwdArgs()
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), q.data_ptr()
+    a.q_stride, a.k_stride = nat.int64x4(q.stride()), nat.int64x4(k.stride())
+    a.v_stride, a.out_stride = nat.int64x4(v.stride()), nat.int64x4(q.stride())
+    a.batch, a.seqlen_q, a.seqlen_k = c["batch"], 1, c["seqlen_k"]
+    a.nheads_q, a.nheads_kv, a.head_dim, a.dtype = c["nheads_q"], c["nheads_kv"], c["head_dim"], nat.TRINIX_BF16
+    ns, wb = ctypes.c_int32(), ctypes.c_int64()
+    nat.check(nat.load_library().trinix_attn_fwd_splitkv_plan(ctypes.byref(a), ctypes.byref(ns), ctypes.byref(wb)),
+              "plan")
+    gbps = kv_bytes / (us * 1e-6) / 1e9
+    # practical ceiling on this box: torch's device copy of the same bytes
+    src = torch.cat([k.view(-1), v.view(-1)])
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    cus = time_events(lambda: dst.copy_(src), 10, torch) * 1e3
+    del src, dst
+    return {"config": "Llama-3-8B decode step: B=16, seqlen_q=1, seqlen_k=8192, 32 q / 8 kv heads, D=128, bf16",
+            "kernels": "attn_decode16 + attn_decode_combine", "num_splits": ns.value,
+            "us_per_step": round(us, 2), "kv_bytes": kv_bytes, "achieved_gbps": round(gbps, 1),
+            "peak_gbps": PEAK_HBM_GBPS, "frac": round(gbps / PEAK_HBM_GBPS, 4),
+            "copy_gbps_same_box": round(2 * kv_bytes / (cus * 1e-6) / 1e9, 1)}
+
+
 def algo_bytes(w):
     """Minimum HBM bytes of one launch: q, k, v read once, out written once
     (+ the mask read once)."""
@@ -301,6 +349,12 @@ def main():
         fb = fwd_bwd_ms(w, inp, torch)
         rec["fwd_bwd"] = {"ms": round(fb, 4), "tflops": round(3.5 * fl / fb / 1e9, 2),
                           "bwd_ms": round(fb - ms, 4), "bwd_tflops": round(2.5 * fl / (fb - ms) / 1e9, 2)}
+    if dname in ("bf16", "fp16"):
+        del inp
+        torch.cuda.empty_cache()
+        rec["decode"] = decode_measure(torch)
+        torch.cuda.empty_cache()
+        inp = None
     if args.all:
         extra = {}
         for name, wo in WORKLOADS.items():
@@ -314,7 +368,7 @@ def main():
             torch.cuda.empty_cache()
         rec["other_workloads"] = extra
     if not args.no_cpu:
-        del inp
+        inp = None
         torch.cuda.empty_cache()
         rec["cpu_baseline"] = cpu_baseline(w, args.cpu_sample_heads, torch)
         rec["speedup_vs_cpu_full_config"] = round(rec["cpu_baseline"]["full_config_ms_extrapolated"] / ms, 1)
