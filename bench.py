@@ -236,6 +236,43 @@ def decode_measure(torch, iters=30):
             "copy_gbps_same_box": round(2 * kv_bytes / (cus * 1e-6) / 1e9, 1)}
 
 
+def layer_measure(torch, iters=10):
+    """The C3 model's attention layer forward (Llama-3-8B GQA: E=4096, 32 q /
+    8 kv heads, RoPE 5e5, causal, qk_norm=True, B=1, S=8192, bf16, inference)
+    with the fused RoPE + qk RMSNorm kernel and with the eager norm modules,
+    plus that kernel alone on q (algorithmic bytes: q read and written once).
+    The projections are torch Linear layers (hipBLASLt GEMMs)."""
+    import trinix_amd as tx
+    from trinix_amd.kernels import qk_rmsnorm
+
+    B, S, H, HKV, D = 1, 8192, 32, 8, 128
+    res = {"config": "GQA layer forward, E=4096, 32 q / 8 kv heads, D=128, B=1, S=8192, RoPE 5e5, causal, "
+                     "qk_norm (RMSNorm), bf16, no grad"}
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(B, S, H * D, device="cuda", generator=g).to(torch.bfloat16)
+    for fused in (True, False):
+        layer = tx.FastGroupedQueryAttention(H * D, H, HKV, causal=True, position_method="rope", rope_base=500000.0,
+                                             qk_norm=True, max_seq_len=S).to("cuda", torch.bfloat16)
+        if not fused:
+            layer._fused_qk_norm_applies = lambda q, k: False
+        with torch.no_grad():
+            for _ in range(3):
+                layer(x)
+            res["us_fused_qk_norm" if fused else "us_eager_qk_norm"] = round(
+                time_events(lambda: layer(x), iters, torch) * 1e3, 1)
+        if fused:
+            q = torch.randn(B, S, H, D, device="cuda", generator=g).to(torch.bfloat16)
+            cos, sin = layer.position_embedding(q, S)
+            w = layer.q_norm.weight.detach()
+            with torch.no_grad():
+                qk_rmsnorm(q, w, 1e-6, cos, sin)
+                us = time_events(lambda: qk_rmsnorm(q, w, 1e-6, cos, sin), 20, torch) * 1e3
+            res["qk_norm_kernel_q_us"] = round(us, 2)
+            res["qk_norm_kernel_q_gbps"] = round(2 * q.numel() * 2 / (us * 1e-6) / 1e9, 1)
+        del layer
+    return res
+
+
 def algo_bytes(w):
     """Minimum HBM bytes of one launch: q, k, v read once, out written once
     (+ the mask read once)."""
@@ -353,6 +390,8 @@ def main():
         del inp
         torch.cuda.empty_cache()
         rec["decode"] = decode_measure(torch)
+        torch.cuda.empty_cache()
+        rec["layer"] = layer_measure(torch)
         torch.cuda.empty_cache()
         inp = None
     if args.all:

@@ -33,6 +33,10 @@
  *                                 returns a detached output (attention_kernel.py:
  *                                 497-517); gradients of the eager path
  *                                 (trinix/layers/attention/base.py:347-400)
+ *   trinix_qk_norm             <- q_norm / k_norm (FastRMSNorm over head_dim) after
+ *                                 RoPE in the layers: base.py:163-176,
+ *                                 grouped_query_attention.py:171-177,
+ *                                 trinix/layers/norm/rmsnorm.py:62-75
  *   trinix_alibi_bias          <- TritonALiBiKernel.apply / FastALiBiPositionEmbedding
  *                                 trinix/kernels/alibi_kernel.py:8-54,93-124,
  *                                 trinix/layers/embeddings/alibi.py:65-90
@@ -167,6 +171,24 @@ int trinix_rope_apply(const void* x, const int64_t x_stride[4], void* out,
                       int32_t dtype, const void* cos, const void* sin,
                       int64_t cs_stride, const int64_t* position_ids,
                       void* stream);
+
+/* qk-norm of the attention layers, fused with RoPE (reference
+ * trinix/layers/attention/base.py:163-176 with FastRMSNorm's PyTorch path
+ * trinix/layers/norm/rmsnorm.py:62-75, applied after RoPE at
+ * grouped_query_attention.py:171-177):
+ *   y   = cos ? rope(x) : x          (as trinix_rope_apply, rounded to dtype)
+ *   out = weight * to_dtype(y * rsqrt(mean_d(y^2) + eps))
+ * bf16/fp16 x, out and weight (head_dim elements, same dtype); head_dim in
+ * {16, 32, 64, 128, 256}; x/out (B, S, H, D) element strides, d stride 1,
+ * 16-byte aligned rows; cos/sin as for trinix_rope_apply.  The fp32 sum of
+ * squares is ordered differently from torch's reduction: an output element
+ * can differ from eager by one ulp of the dtype, rarely. */
+int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* out,
+                   const int64_t out_stride[4], int64_t batch, int64_t seqlen,
+                   int64_t nheads, int64_t head_dim, int32_t dtype,
+                   const void* weight, float eps, const void* cos,
+                   const void* sin, int64_t cs_stride,
+                   const int64_t* position_ids, void* stream);
 
 /* Backward of trinix_attn_fwd for bf16/fp16 without dropout.  No
  * counterpart in the reference (its Triton attention has no backward,

@@ -24,6 +24,11 @@ path the north star names as the parity target, the eager
   additive mask as ``(1 - w) * -inf``, which is NaN on allowed positions
   (0 * -inf); here allowed -> 0, disallowed -> -inf, for the functional
   window ``-wl <= j - i <= wr`` (trinix/kernels/attention_kernel.py:132-135).
+* ``qk_rms_norm``      <- ``FastRMSNorm._pytorch_forward``
+  (trinix/layers/norm/rmsnorm.py:62-75), the qk-norm over head_dim the
+  layers build at base.py:163-176 and apply after RoPE
+  (grouped_query_attention.py:171-177); head_dim <= 2048 always takes this
+  path in the reference.
 * ``functional_attention`` composes them the way the layers feed the eager
   path: window mask + user mask + ALiBi bias summed in fp32
   (base.py:309-319) and added into the q.dtype scores (base.py:392).
@@ -131,6 +136,15 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
         c = cos[position_ids].unsqueeze(2)
         s = sin[position_ids].unsqueeze(2)
     return x * c + _rotate_half(x) * s
+
+
+def qk_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """weight * (x.float() * rsqrt(mean(x.float()**2, -1) + eps)).to(x.dtype),
+    in the reference's op order (rmsnorm.py:70-75)."""
+    dt = x.dtype
+    h = x.to(torch.float32)
+    h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * h.to(dt)
 
 
 def alibi_slopes(num_heads: int) -> torch.Tensor:

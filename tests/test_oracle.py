@@ -218,3 +218,23 @@ def test_c5_block_mask_properties():
     assert torch.equal(full, blocks.any(-1))  # blocks are all -inf or all 0
     assert 0.05 < full.float().mean().item() < 0.15
     assert (~full).any(dim=1).all()  # every block-row keeps an open block
+
+
+def test_qk_rms_norm_pinned():
+    """The qk RMSNorm restatement against an fp64 per-row loop, the closed
+    form of a constant row, and scale invariance (eps = 0)."""
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(2, 3, 4, 16, generator=g)
+    w = torch.randn(16, generator=g)
+    y = orc.qk_rms_norm(x, w, 1e-6)
+    xd, wd = x.double().numpy(), w.double().numpy()
+    for idx in np.ndindex(2, 3, 4):
+        row = xd[idx]
+        want = wd * row / math.sqrt(sum(v * v for v in row) / 16 + 1e-6)
+        assert np.allclose(y[idx].double().numpy(), want, rtol=2e-6, atol=1e-7)
+    c = torch.full((1, 1, 1, 16), -3.0)
+    assert torch.allclose(orc.qk_rms_norm(c, w, 0.0), -w, rtol=1e-6)
+    assert torch.allclose(orc.qk_rms_norm(7.5 * x, w, 0.0), orc.qk_rms_norm(x, w, 0.0), rtol=1e-5, atol=1e-6)
+    yb = orc.qk_rms_norm(x.bfloat16(), w.bfloat16(), 1e-6)
+    assert yb.dtype == torch.bfloat16
+    assert (yb.float() - y).abs().max() <= 2 ** -6 * y.abs().max()

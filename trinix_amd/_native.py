@@ -152,6 +152,11 @@ SIGNATURES = {
     "trinix_attn_fwd_splitkv_plan": (c_int32, [POINTER(AttnFwdArgs), POINTER(c_int32), POINTER(c_int64)]),
     "trinix_attn_fwd_splitkv": (c_int32, [POINTER(AttnFwdArgs), c_void_p, c_int64, c_void_p]),
     "trinix_attn_bwd": (c_int32, [POINTER(AttnBwdArgs), c_void_p]),
+    "trinix_qk_norm": (
+        c_int32,
+        [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64, c_int32,
+         c_void_p, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
+    ),
     "trinix_alibi_bias": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "trinix_attn_tile_config": (c_int32, [c_int64, c_int32, POINTER(TileCfg)]),
     "trinix_attn_is_available": (c_int32, []),

@@ -288,6 +288,22 @@ class FastBaseAttention(nn.Module):
             attn_mask = self._apply_sliding_window_mask(attn_mask, k.shape[1], q.device, q.shape[1])
         return self._apply_pytorch_attention(q, k, v, attn_mask)
 
+    def _fused_qk_norm_applies(self, q, k) -> bool:
+        """qk RMSNorm (+ RoPE) through the fused kernel: GPU kernel path,
+        RMSNorm weights in the activations' 16-bit dtype, a supported
+        head_dim, RoPE / ALiBi / no position encoding, and no gradient needed
+        (the fused kernel has no backward; training keeps the eager modules)."""
+        if not (self.qk_norm and isinstance(self.q_norm, _QKRMSNorm) and self._uses_kernel(q)):
+            return False
+        if self.position_method not in ("rope", "alibi", "none"):
+            return False
+        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or self.q_norm.weight.requires_grad
+                                        or self.k_norm.weight.requires_grad):
+            return False
+        from ...kernels.qk_norm_kernel import qk_norm_supported
+
+        return qk_norm_supported(q, self.q_norm.weight) and qk_norm_supported(k, self.k_norm.weight)
+
     # -- shared layer body ------------------------------------------------------
     def _attend(self, q, k, v, attention_mask, position_ids, past_key_value, use_zero_attn):
         """q (B, Sq, H, D), k/v (B, Sk, Hkv, D) after projection.  Returns
@@ -298,6 +314,7 @@ class FastBaseAttention(nn.Module):
         fuse_rope = (self.position_method == "rope" and self.position_embedding is not None and q.is_cuda
                      and self._uses_kernel(q) and position_ids is None and not self.qk_norm
                      and past_key_value is None and not (use_zero_attn and self.add_zero_attn))
+        fuse_norm = self._fused_qk_norm_applies(q, k)
         if fuse_rope:
             # q is rotated inside the attention kernel; k by the RoPE kernel
             # (it is also the returned cache).
@@ -306,13 +323,24 @@ class FastBaseAttention(nn.Module):
 
             k = rotate(k, cos, sin)
             rotary = (cos, sin)
+        elif fuse_norm:
+            # RoPE (if any) and the qk RMSNorm in one kernel pass per tensor
+            # (the eager order: rotate, then normalise).
+            from ...kernels.qk_norm_kernel import qk_rmsnorm
+
+            cos = sin = None
+            if self.position_method == "rope" and self.position_embedding is not None:
+                cos, sin = self.position_embedding(q, max(seq_len_q, seq_len_k))
+            q = qk_rmsnorm(q, self.q_norm.weight, self.q_norm.eps, cos, sin, position_ids)
+            k = qk_rmsnorm(k, self.k_norm.weight, self.k_norm.eps, cos, sin, position_ids)
+            attention_mask = self._merge_position_bias(attention_mask, None)
         else:
             q, k, position_bias = self._apply_position_embedding(q, k, seq_len_q, seq_len_k, bs, position_ids)
             attention_mask = self._merge_position_bias(attention_mask, position_bias)
         q = q.transpose(1, 2)
         k = k.transpose(1, 2)
         v = v.transpose(1, 2)
-        if self.qk_norm:
+        if self.qk_norm and not fuse_norm:
             q = self.q_norm(q)
             k = self.k_norm(k)
         if past_key_value is not None:
