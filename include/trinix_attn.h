@@ -60,7 +60,7 @@ typedef enum trinix_status {
   TRINIX_OK = 0,
   TRINIX_ERR_NULL_POINTER = 1,   /* a required pointer is NULL             */
   TRINIX_ERR_BAD_DTYPE = 2,      /* unsupported dtype / dtype mismatch      */
-  TRINIX_ERR_BAD_HEAD_DIM = 3,   /* head_dim not in {64, 128}               */
+  TRINIX_ERR_BAD_HEAD_DIM = 3,   /* head_dim not built for the entry point (forward: 64, 128, 256; backward, split-KV: 64, 128) */
   TRINIX_ERR_BAD_SHAPE = 4,      /* non-positive or inconsistent sizes      */
   TRINIX_ERR_BAD_STRIDE = 5,     /* d-stride != 1, misaligned rows, or a 16-bit K/V key-row stride >= 2^22 elements */
   TRINIX_ERR_BAD_ARGUMENT = 6,   /* other invalid argument (dropout, ...)   */

@@ -69,6 +69,8 @@ def test_version_status_and_tiles(lib):
     assert lib.trinix_attn_tile_config(128, nat.TRINIX_BF16, ctypes.byref(cfg)) == 0
     assert cfg.block_d == 128 and cfg.block_m % 32 == 0 and cfg.block_n % 64 == 0
     assert lib.trinix_attn_tile_config(96, nat.TRINIX_BF16, ctypes.byref(cfg)) == nat.TRINIX_ERR_BAD_HEAD_DIM
+    assert lib.trinix_attn_tile_config(256, nat.TRINIX_BF16, ctypes.byref(cfg)) == 0
+    assert cfg.block_d == 256 and cfg.lds_bytes == 4 * 64 * 256 * 2
     assert lib.trinix_attn_tile_config(64, 9, ctypes.byref(cfg)) == nat.TRINIX_ERR_BAD_DTYPE
 
 
@@ -135,7 +137,8 @@ def test_functional_api_errors_match_reference():
 def test_kernel_head_dim_padding_rule():
     from trinix_amd.kernels.attention_kernel import kernel_head_dim
 
-    assert [kernel_head_dim(d) for d in (8, 32, 64, 65, 80, 128, 129)] == [64, 64, 64, 128, 128, 128, None]
+    assert [kernel_head_dim(d) for d in (8, 32, 64, 65, 80, 128, 129, 192, 256, 257)] == \
+        [64, 64, 64, 128, 128, 128, 256, 256, 256, None]
 
 
 def _plan(lib, **kw):

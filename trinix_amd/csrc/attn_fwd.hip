@@ -275,11 +275,11 @@ int check_tensor(const void* ptr, const int64_t st[4], int esize) {
 }
 
 // Tile configuration of the 16-bit kernel: 4 wavefronts x 32 query rows,
-// 64-key tiles, 2 wavefronts per SIMD.  TRINIX_ATTN_CFG="nw,occ,bn" overrides the choice (tuning
-// only; a configuration that is not built is rejected with
-// TRINIX_ERR_BAD_ARGUMENT).
-Cfg16 pick_cfg16(int64_t batch, int64_t hq, int64_t sq) {
-  Cfg16 c{4, 2, 64};
+// 64-key tiles, 2 wavefronts per SIMD (1 for head_dim 256).
+// TRINIX_ATTN_CFG="nw,occ,bn" overrides the choice (tuning only; a
+// configuration that is not built is rejected with TRINIX_ERR_BAD_ARGUMENT).
+Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq) {
+  Cfg16 c{4, head_dim == 256 ? 1 : 2, 64};
   (void)batch;
   (void)hq;
   (void)sq;
@@ -298,7 +298,7 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (!a) return TRINIX_ERR_NULL_POINTER;
   const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
   if (a->dtype != TRINIX_F32 && a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
   if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0)
     return TRINIX_ERR_BAD_SHAPE;
   if (a->nheads_q % a->nheads_kv != 0) return TRINIX_ERR_BAD_SHAPE;
@@ -338,7 +338,7 @@ const char* trinix_status_string(int status) {
     case TRINIX_OK: return "ok";
     case TRINIX_ERR_NULL_POINTER: return "a required pointer is NULL";
     case TRINIX_ERR_BAD_DTYPE: return "unsupported dtype";
-    case TRINIX_ERR_BAD_HEAD_DIM: return "unsupported head_dim (kernels are built for 64 and 128)";
+    case TRINIX_ERR_BAD_HEAD_DIM: return "unsupported head_dim (forward kernels are built for 64, 128 and 256; backward for 64 and 128)";
     case TRINIX_ERR_BAD_SHAPE: return "invalid or inconsistent sizes";
     case TRINIX_ERR_BAD_STRIDE: return "unsupported strides or alignment (head_dim stride must be 1, 16-byte aligned rows, 16-bit K/V key-row stride below 2^22 elements)";
     case TRINIX_ERR_BAD_ARGUMENT: return "invalid argument";
@@ -360,9 +360,9 @@ int trinix_attn_is_available(void) {
 
 int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* out) {
   if (!out) return TRINIX_ERR_NULL_POINTER;
-  if (head_dim != 64 && head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
   if (dtype == TRINIX_BF16 || dtype == TRINIX_F16) {
-    const Cfg16 c = pick_cfg16(1 << 20, 1, 1 << 20);  // large-problem choice
+    const Cfg16 c = pick_cfg16(head_dim, 1 << 20, 1, 1 << 20);  // large-problem choice
     out->block_m = 32 * c.nw;
     out->block_n = c.bn;
     out->block_d = (int32_t)head_dim;
@@ -401,7 +401,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.Hkv = (int)a->nheads_kv;
   p.G = p.Hq / p.Hkv;
   const bool f32 = a->dtype == TRINIX_F32;
-  const Cfg16 cfg = pick_cfg16(a->batch, a->nheads_q, a->seqlen_q);
+  const Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q);
   const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw;
   p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
   const int64_t total = (int64_t)p.B * p.Hq * p.num_mblk;
@@ -442,14 +442,18 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   if (f32) {
     const dim3 grid((unsigned)p.total_work), block(kWavesF32 * 64);
     if (a->head_dim == 64) hipLaunchKernelGGL((attn_fwd_f32<64, kWavesF32>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((attn_fwd_f32<128, kWavesF32>), grid, block, 0, st, p);
+    else if (a->head_dim == 128) hipLaunchKernelGGL((attn_fwd_f32<128, kWavesF32>), grid, block, 0, st, p);
+    else hipLaunchKernelGGL((attn_fwd_f32<256, kWavesF32>), grid, block, 0, st, p);
     err = hipGetLastError();
   } else {
     const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0);
-    if (a->dtype == TRINIX_BF16)
-      err = a->head_dim == 64 ? launch_attn16_bf16_d64(p, cfg, feat, st) : launch_attn16_bf16_d128(p, cfg, feat, st);
+    const bool bf = a->dtype == TRINIX_BF16;
+    if (a->head_dim == 64)
+      err = bf ? launch_attn16_bf16_d64(p, cfg, feat, st) : launch_attn16_f16_d64(p, cfg, feat, st);
+    else if (a->head_dim == 128)
+      err = bf ? launch_attn16_bf16_d128(p, cfg, feat, st) : launch_attn16_f16_d128(p, cfg, feat, st);
     else
-      err = a->head_dim == 64 ? launch_attn16_f16_d64(p, cfg, feat, st) : launch_attn16_f16_d128(p, cfg, feat, st);
+      err = bf ? launch_attn16_bf16_d256(p, cfg, feat, st) : launch_attn16_f16_d256(p, cfg, feat, st);
     if (err == hipErrorInvalidValue) return TRINIX_ERR_BAD_ARGUMENT;  // tile config not built
   }
   return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;

@@ -244,7 +244,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // K fragments are read KPF MFMAs ahead; the sched_group_barriers keep the
   // reads ahead of their MFMAs instead of letting each MFMA wait on its read.
   constexpr int NQK = NB * DS;
-  constexpr int KPF = MASK ? 3 : 6;  // mask kernels hold more live values: shorter read-ahead
+  // mask kernels (and D = 256, with 192 registers of Q and O) hold more live
+  // values: shorter read-ahead
+  constexpr int KPF = D == 256 ? 2 : (MASK ? 3 : 6);
   // Byte offset of K fragment (nb, ds) of this lane in a K tile: row
   // nb*32 + r, unit (2ds + g) ^ swz_k(r) (the swizzle depends only on r).  As
   // 16*((2ds) ^ (g ^ swz)) = 32*ds ^ 16*(g ^ swz) and the row offset has no
@@ -308,7 +310,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
   constexpr int NPV = DB * NB * 2;
-  constexpr int VPF = MASK ? 2 : 4;
+  constexpr int VPF = D == 256 ? 2 : (MASK ? 2 : 4);
   // vpre: the first VPF fragments, read ahead (before the softmax) by the caller.
   auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2], const u32x4_t(&vpre)[VPF]) __attribute__((always_inline)) {
     u32x4_t vf[NPV];
@@ -540,11 +542,14 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   }
 }
 
-// Tile config built for every (dtype, D): (nw, occ, bn) = (4, 2, 64), every
-// feature combination.
+// Tile config built per (dtype, D), every feature combination:
+// (nw, occ, bn) = (4, 2, 64) for D <= 128; (4, 1, 64) for D = 256, whose Q
+// fragment (64 VGPRs) and O accumulator (128) need one wavefront per SIMD,
+// and whose double-buffered K/V tiles take 128 KiB of LDS.
 #define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                              \
   hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                           \
-    if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == 2) return launch_feat<E, D, 64, 4, 2>(p, feat, st);  \
+    constexpr int kOcc = (D) == 256 ? 1 : 2;                                                          \
+    if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == kOcc) return launch_feat<E, D, 64, 4, kOcc>(p, feat, st); \
     return hipErrorInvalidValue;                                                                        \
   }
 

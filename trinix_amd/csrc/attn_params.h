@@ -83,6 +83,8 @@ hipError_t launch_attn16_bf16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipSt
 hipError_t launch_attn16_bf16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 hipError_t launch_attn16_f16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 hipError_t launch_attn16_f16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
+hipError_t launch_attn16_bf16_d256(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
+hipError_t launch_attn16_f16_d256(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 
 // Host-side argument checks of trinix_attn_fwd (no launch); also applied by
 // the split-KV entry points.

@@ -13,14 +13,16 @@ typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
 // Swizzle of the 16-byte units of a D-wide row-major tile row.  K rows are
 // read 16 bytes per lane, 16 consecutive rows per access; V rows are read 8
 // bytes per lane by ds_read_b64_tr_b16, 4 consecutive rows x 64 bytes per
-// 32 lanes.
+// 32 lanes.  Rows of D >= 128 (256 or 512 bytes) all start on bank 0, so
+// the unit index is XORed with the row (mod 16 units); 128-byte rows (D = 64)
+// pair up first.
 template <int D>
 __device__ inline int swz_k(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+  return D >= 128 ? (row & 15) : ((row >> 1) & 7);
 }
 template <int D>
 __device__ inline int swz_v(int row) {
-  return D == 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
+  return D >= 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
 }
 
 // Asynchronous global -> LDS copy (global_load_lds_dwordx4): lane l's 16

@@ -42,7 +42,9 @@ _MASK_DTYPE_CODE = {
     torch.bfloat16: nat.TRINIX_BF16,
     torch.uint8: nat.TRINIX_U8,
 }
-KERNEL_HEAD_DIMS = (64, 128)
+KERNEL_HEAD_DIMS = (64, 128, 256)
+# The backward kernels are built for these (the forward for all of the above).
+BACKWARD_HEAD_DIMS = (64, 128)
 
 
 # Calls with at most this many query rows (bf16/fp16, no dropout) go to the
@@ -240,7 +242,8 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
 
     # Decode-shaped calls (few query rows, long KV) take the split-KV kernel;
     # it has no fused RoPE, so q is rotated here first.
-    split_kv = SPLITKV_ENABLED and Sq <= SPLITKV_MAX_SQ and q.dtype != torch.float32 and dropout_p == 0.0
+    split_kv = (SPLITKV_ENABLED and Sq <= SPLITKV_MAX_SQ and q.dtype != torch.float32 and dropout_p == 0.0
+                and d_kernel <= 128)
     if split_kv and rotary_cos is not None:
         from .rope_kernel import rope_apply
         q = rope_apply(q, rotary_cos, rotary_sin)
@@ -424,27 +427,28 @@ _warned_no_grad = set()
 def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, window_size=None, alibi_slopes=None,
               *, rotary_cos=None, rotary_sin=None, rotary_k=True, return_lse=False):
     """Attention with gradients when q, k or v require them (bf16/fp16, no
-    dropout); otherwise, and in those cases, ``TritonAttentionKernel.apply``.
+    dropout, head_dim <= 128); otherwise ``TritonAttentionKernel.apply``.
 
     The reference's Triton attention has no backward (its output is detached,
     ``attention_kernel.py:497-517``).  Here bf16/fp16 attention without
-    dropout is differentiable through ``trinix_attn_bwd``.  fp32 or dropout
-    with gradients required keep the reference's behaviour, a detached
-    output, and warn once.
+    dropout and with head_dim <= 128 is differentiable through
+    ``trinix_attn_bwd``.  fp32, dropout or head_dim > 128 with gradients
+    required keep the reference's behaviour, a detached output, and warn once.
     """
     needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
     if needs_grad:
-        if q.dtype in (torch.float16, torch.bfloat16) and dropout_p == 0.0:
+        dk = kernel_head_dim(q.shape[-1])
+        if q.dtype in (torch.float16, torch.bfloat16) and dropout_p == 0.0 and dk in BACKWARD_HEAD_DIMS:
             if scale is None:
                 scale = q.shape[-1] ** -0.5
             return _HipAttnFunction.apply(q, k, v, attn_mask, causal, scale, window_size, alibi_slopes, rotary_cos,
                                           rotary_sin, rotary_k, return_lse)
-        key = (q.dtype, dropout_p > 0.0)
+        key = (q.dtype, dropout_p > 0.0, dk)
         if key not in _warned_no_grad:
             _warned_no_grad.add(key)
-            warnings.warn("HIP attention backward runs in bf16/fp16 without dropout; this call's output is "
-                          "detached (no gradient flows through it), as in the reference Triton path",
-                          stacklevel=2)
+            warnings.warn("HIP attention backward runs in bf16/fp16 without dropout, head_dim <= 128; this "
+                          "call's output is detached (no gradient flows through it), as in the reference "
+                          "Triton path", stacklevel=2)
     return TritonAttentionKernel.apply(q, k, v, attn_mask=attn_mask, causal=causal, scale=scale, dropout_p=dropout_p,
                                        window_size=window_size, alibi_slopes=alibi_slopes, rotary_cos=rotary_cos,
                                        rotary_sin=rotary_sin, rotary_k=rotary_k, return_lse=return_lse)
