@@ -250,15 +250,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // Byte offset of K fragment (nb, ds) of this lane in a K tile: row
   // nb*32 + r, unit (2ds + g) ^ swz_k(r) (the swizzle depends only on r).  As
   // 16*((2ds) ^ (g ^ swz)) = 32*ds ^ 16*(g ^ swz) and the row offset has no
-  // bits below bit 8, it is nb*32*D*2 + (k_lane ^ 32*ds): one register, one
-  // v_xor per read (kept at the read by the empty asm, instead of eight
-  // loop-invariant addresses held in registers).
+  // bits below bit 8, it is nb*32*D*2 + (k_lane ^ 32*ds).  The DS XOR values
+  // are loop-invariant and live in registers; each read uses one directly,
+  // with nb's row offset in the instruction's immediate.
   const uint32_t k_lane = (uint32_t)(r * D * 2 + 16 * (g ^ swz_k<D>(r)));
   auto qk = [&](const uint16_t* kt, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
     auto kread = [&](int k) __attribute__((always_inline)) {
       const int nb = k / DS, ds = k % DS;
-      uint32_t off = k_lane ^ (uint32_t)(ds << 5);
-      asm volatile("" : "+v"(off));
+      const uint32_t off = k_lane ^ (uint32_t)(ds << 5);
       return *(const u32x4_t*)((const char*)kt + nb * 32 * D * 2 + off);
     };
     u32x4_t kf[NQK];
@@ -424,15 +423,16 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
                                E::pack(s[nb][kk * 8 + 4], s[nb][kk * 8 + 5]), E::pack(s[nb][kk * 8 + 6], s[nb][kk * 8 + 7])};
     if constexpr (!DROP) {
       // Row sum of the rounded P the PV product uses, two elements per
-      // v_dot2 (x.lo*1 + x.hi*1 + acc), four independent accumulators.
-      float r4[4] = {0.f, 0.f, 0.f, 0.f};
+      // v_dot2 (x.lo*1 + x.hi*1 + acc), two independent accumulators, the
+      // first one seeded with the running sum.
+      float r2[2] = {l_run, 0.f};
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) r4[e] = E::dot2_ones(pb[nb][kk][e], r4[e]);
-      l_run += (r4[0] + r4[1]) + (r4[2] + r4[3]);
+          for (int e = 0; e < 4; ++e) r2[e & 1] = E::dot2_ones(pb[nb][kk][e], r2[e & 1]);
+      l_run = r2[0] + r2[1];
     }
   };
 
