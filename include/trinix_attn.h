@@ -164,13 +164,17 @@ int trinix_attn_mask_blockmap(const void* mask, int32_t mask_dtype,
  * with every product and the sum rounded to the tensor dtype, as eager
  * PyTorch does.  x, out: (B, S, H, D) with strides (d stride 1); cos/sin:
  * rows of >= D/2 entries in x's dtype with row stride `cs_stride`; row
- * index = position_ids[b*S + s] (int64) if position_ids != NULL, else s. */
+ * index = position_ids[b*S + s] (int64) if position_ids != NULL, else s.
+ * `cs_rows` is the number of table rows (>= seqlen without position_ids);
+ * position ids outside [0, cs_rows) are clamped into it, so no id reads
+ * outside the tables (host wrappers reject such ids where they can read
+ * them, i.e. outside graph capture). */
 int trinix_rope_apply(const void* x, const int64_t x_stride[4], void* out,
                       const int64_t out_stride[4], int64_t batch,
                       int64_t seqlen, int64_t nheads, int64_t head_dim,
                       int32_t dtype, const void* cos, const void* sin,
-                      int64_t cs_stride, const int64_t* position_ids,
-                      void* stream);
+                      int64_t cs_stride, int64_t cs_rows,
+                      const int64_t* position_ids, void* stream);
 
 /* qk-norm of the attention layers, fused with RoPE (reference
  * trinix/layers/attention/base.py:163-176 with FastRMSNorm's PyTorch path
@@ -180,14 +184,15 @@ int trinix_rope_apply(const void* x, const int64_t x_stride[4], void* out,
  *   out = weight * to_dtype(y * rsqrt(mean_d(y^2) + eps))
  * bf16/fp16 x, out and weight (head_dim elements, same dtype); head_dim in
  * {16, 32, 64, 128, 256}; x/out (B, S, H, D) element strides, d stride 1,
- * 16-byte aligned rows; cos/sin as for trinix_rope_apply.  The fp32 sum of
+ * 16-byte aligned rows; cos/sin/cs_rows/position_ids as for
+ * trinix_rope_apply.  The fp32 sum of
  * squares is ordered differently from torch's reduction: an output element
  * can differ from eager by one ulp of the dtype, rarely. */
 int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* out,
                    const int64_t out_stride[4], int64_t batch, int64_t seqlen,
                    int64_t nheads, int64_t head_dim, int32_t dtype,
                    const void* weight, float eps, const void* cos,
-                   const void* sin, int64_t cs_stride,
+                   const void* sin, int64_t cs_stride, int64_t cs_rows,
                    const int64_t* position_ids, void* stream);
 
 /* Backward of trinix_attn_fwd for bf16/fp16 without dropout.  No

@@ -192,7 +192,7 @@ def test_qk_norm_rejects_before_launch(lib):
     st = (ctypes.c_int64 * 4)(8 * 64 * 128, 8 * 128, 128, 1)
 
     def call(x=4096, out=4096, w=4096, D=128, dtype=nat.TRINIX_BF16, stride=st, cos=None, sin=None):
-        return lib.trinix_qk_norm(x, stride, out, stride, 1, 64, 8, D, dtype, w, 1e-6, cos, sin, 64, None, None)
+        return lib.trinix_qk_norm(x, stride, out, stride, 1, 64, 8, D, dtype, w, 1e-6, cos, sin, 64, 64, None, None)
 
     assert call(D=96) == nat.TRINIX_ERR_BAD_HEAD_DIM
     assert call(dtype=nat.TRINIX_F32) == nat.TRINIX_ERR_BAD_DTYPE
@@ -200,3 +200,8 @@ def test_qk_norm_rejects_before_launch(lib):
     assert call(cos=4096) == nat.TRINIX_ERR_NULL_POINTER
     assert call(x=4100) == nat.TRINIX_ERR_BAD_STRIDE
     assert call(stride=(ctypes.c_int64 * 4)(8 * 64 * 128, 8 * 128, 130, 1)) == nat.TRINIX_ERR_BAD_STRIDE
+    # tables shorter than the sequence (no position ids)
+    assert lib.trinix_qk_norm(4096, st, 4096, st, 1, 64, 8, 128, nat.TRINIX_BF16, 4096, 1e-6, 4096, 4096, 64, 63,
+                              None, None) == nat.TRINIX_ERR_BAD_SHAPE
+    assert lib.trinix_rope_apply(4096, st, 4096, st, 1, 64, 8, 128, nat.TRINIX_BF16, 4096, 4096, 64, 63,
+                                 None, None) == nat.TRINIX_ERR_BAD_SHAPE

@@ -1,0 +1,99 @@
+"""HIP graph capture of the attention paths (serving loops capture decode
+steps).  Every entry point enqueues its kernels on the caller's stream and
+allocates nothing itself; the host layer's only device-to-host read (the
+position_ids range check) is skipped while a stream is capturing, and the
+kernels clamp ids to the tables instead.
+
+Each captured graph is replayed several times with new input values copied
+into its static inputs, eager work and synchronisations between replays, and
+every replay is compared with the eager call on the same values (bitwise:
+the same kernels run).
+"""
+import pytest
+import torch
+
+import trinix_amd as tx
+from trinix_amd import triton_attn_func
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def capture(fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    return g, out
+
+
+def replay_and_check(g, static_out, inputs, fn, rounds=3):
+    for rnd in range(rounds):
+        gen = torch.Generator(device=DEV).manual_seed(1000 + rnd)
+        for t in inputs:
+            t.copy_(torch.randn(t.shape, device=DEV, generator=gen).to(t.dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        _ = torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)  # eager work between replays
+        torch.cuda.synchronize()
+        ref = fn()
+        outs = static_out if isinstance(static_out, (tuple, list)) else (static_out,)
+        refs = ref if isinstance(ref, (tuple, list)) else (ref,)
+        for o, r in zip(outs, refs):
+            assert torch.equal(o, r), f"replay {rnd} differs from eager"
+
+
+def test_graph_prefill_gqa_fused_rope():
+    B, S, H, HKV, D = 1, 512, 8, 2, 128
+    q = torch.zeros(B, S, H, D, device=DEV, dtype=torch.bfloat16)
+    k = torch.zeros(B, S, HKV, D, device=DEV, dtype=torch.bfloat16)
+    v = torch.zeros(B, S, HKV, D, device=DEV, dtype=torch.bfloat16)
+    emb = tx.FastRoPEPositionEmbedding(D, max_position_embeddings=S, base=500000.0).to(DEV)
+    cos, sin = emb(q, S)
+
+    def fn():
+        return triton_attn_func(q, k, v, causal=True, rotary_cos=cos, rotary_sin=sin)
+
+    g, out = capture(fn)
+    replay_and_check(g, out, [q, k, v], fn)
+
+
+def test_graph_decode_split_kv_with_lse():
+    B, Sk, H, HKV, D = 2, 3000, 16, 4, 128
+    q = torch.zeros(B, 1, H, D, device=DEV, dtype=torch.bfloat16)
+    k = torch.zeros(B, Sk, HKV, D, device=DEV, dtype=torch.bfloat16)
+    v = torch.zeros(B, Sk, HKV, D, device=DEV, dtype=torch.bfloat16)
+
+    def fn():
+        return triton_attn_func(q, k, v, return_lse=True)
+
+    g, out = capture(fn)
+    replay_and_check(g, out, [q, k, v], fn)
+
+
+def test_graph_layer_decode_step_with_cache_rope_and_qk_norm():
+    torch.manual_seed(5)
+    E, H, HKV, P = 1024, 8, 2, 100
+    layer = tx.FastGroupedQueryAttention(E, H, HKV, position_method="rope", rope_base=10000.0, qk_norm=True,
+                                         max_seq_len=256).to(DEV, torch.bfloat16).eval()
+    D = E // H
+    past_k = torch.zeros(1, HKV, P, D, device=DEV, dtype=torch.bfloat16)
+    past_v = torch.zeros(1, HKV, P, D, device=DEV, dtype=torch.bfloat16)
+    x = torch.zeros(1, 1, E, device=DEV, dtype=torch.bfloat16)
+    # the layer's RoPE table covers this step's tokens only (reference
+    # rope.py:69-79 builds it for seq_len rows), so a one-token step uses row 0
+    pos = torch.zeros((1, 1), device=DEV, dtype=torch.int64)
+
+    def fn():
+        with torch.no_grad():
+            out, (kc, vc) = layer(x, position_ids=pos, past_key_value=(past_k, past_v), use_cache=True)
+        return out, kc, vc
+
+    g, outs = capture(fn)
+    replay_and_check(g, outs, [x, past_k, past_v], fn)

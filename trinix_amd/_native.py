@@ -147,7 +147,7 @@ SIGNATURES = {
     "trinix_rope_apply": (
         c_int32,
         [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64,
-         c_int32, c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
+         c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p],
     ),
     "trinix_attn_fwd_splitkv_plan": (c_int32, [POINTER(AttnFwdArgs), POINTER(c_int32), POINTER(c_int64)]),
     "trinix_attn_fwd_splitkv": (c_int32, [POINTER(AttnFwdArgs), c_void_p, c_int64, c_void_p]),
@@ -155,7 +155,7 @@ SIGNATURES = {
     "trinix_qk_norm": (
         c_int32,
         [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64, c_int32,
-         c_void_p, c_float, c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
+         c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p],
     ),
     "trinix_alibi_bias": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "trinix_attn_tile_config": (c_int32, [c_int64, c_int32, POINTER(TileCfg)]),

@@ -27,7 +27,7 @@ __global__ __launch_bounds__(256) void qk_norm_kernel(const uint16_t* x, int64_t
                                                       uint16_t* out, int64_t osb, int64_t oss, int64_t osh, int S,
                                                       int H, int D, const uint16_t* w, float eps,
                                                       const uint16_t* cosp, const uint16_t* sinp, int64_t cs,
-                                                      const int64_t* pos, int64_t rows) {
+                                                      int64_t cs_rows, const int64_t* pos, int64_t rows) {
 #pragma clang fp contract(off)
   const int nch = D / 16;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -45,7 +45,9 @@ __global__ __launch_bounds__(256) void qk_norm_kernel(const uint16_t* x, int64_t
   const u32x4_t x2 = *(const u32x4_t*)(xr + d + half);
   float y1[8], y2[8];
   if (cosp) {
-    const int64_t ps = pos ? pos[(int64_t)b * S + s] : s;
+    // position ids are clamped to the table (the host rejects out-of-range
+    // ids except while a graph is being captured, when it cannot read them)
+    const int64_t ps = pos ? min(max(pos[(int64_t)b * S + s], (int64_t)0), cs_rows - 1) : s;
     const u32x4_t cw = *(const u32x4_t*)(cosp + ps * cs + d);
     const u32x4_t sw = *(const u32x4_t*)(sinp + ps * cs + d);
 #pragma unroll
@@ -96,7 +98,7 @@ using namespace trinix;
 extern "C" int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* out, const int64_t out_stride[4],
                               int64_t batch, int64_t seqlen, int64_t nheads, int64_t head_dim, int32_t dtype,
                               const void* weight, float eps, const void* cos, const void* sin, int64_t cs_stride,
-                              const int64_t* position_ids, void* stream) {
+                              int64_t cs_rows, const int64_t* position_ids, void* stream) {
   if (!x || !out || !x_stride || !out_stride || !weight) return TRINIX_ERR_NULL_POINTER;
   if (dtype != TRINIX_BF16 && dtype != TRINIX_F16) return TRINIX_ERR_BAD_DTYPE;
   if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
@@ -111,6 +113,7 @@ extern "C" int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* ou
     if (x_stride[a] % 8 != 0 || out_stride[a] % 8 != 0) return TRINIX_ERR_BAD_STRIDE;
   if (cos && (!aligned16_ptr(cos) || !aligned16_ptr(sin) || cs_stride % 8 != 0 || cs_stride < head_dim / 2))
     return TRINIX_ERR_BAD_STRIDE;
+  if (cos && cs_rows < (position_ids ? 1 : seqlen)) return TRINIX_ERR_BAD_SHAPE;
   const int64_t rows = batch * seqlen * nheads;
   const int64_t threads = rows * (head_dim / 16);
   const int64_t blocks = (threads + 255) / 256;
@@ -122,11 +125,11 @@ extern "C" int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* ou
     hipLaunchKernelGGL(qk_norm_kernel<BF16>, grid, block, 0, st, (const uint16_t*)x, x_stride[0], x_stride[1],
                        x_stride[2], (uint16_t*)out, out_stride[0], out_stride[1], out_stride[2], (int)seqlen,
                        (int)nheads, (int)head_dim, (const uint16_t*)weight, eps, (const uint16_t*)cos,
-                       (const uint16_t*)sin, cs_stride, position_ids, rows);
+                       (const uint16_t*)sin, cs_stride, cs_rows, position_ids, rows);
   else
     hipLaunchKernelGGL(qk_norm_kernel<F16>, grid, block, 0, st, (const uint16_t*)x, x_stride[0], x_stride[1],
                        x_stride[2], (uint16_t*)out, out_stride[0], out_stride[1], out_stride[2], (int)seqlen,
                        (int)nheads, (int)head_dim, (const uint16_t*)weight, eps, (const uint16_t*)cos,
-                       (const uint16_t*)sin, cs_stride, position_ids, rows);
+                       (const uint16_t*)sin, cs_stride, cs_rows, position_ids, rows);
   return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }

@@ -18,8 +18,8 @@ template <class E>
 __global__ __launch_bounds__(256) void rope16_kernel(const uint16_t* x, int64_t xsb, int64_t xss, int64_t xsh,
                                                      uint16_t* out, int64_t osb, int64_t oss, int64_t osh,
                                                      int S, int H, int D, const uint16_t* cosp,
-                                                     const uint16_t* sinp, int64_t cs, const int64_t* pos,
-                                                     int64_t total) {
+                                                     const uint16_t* sinp, int64_t cs, int64_t cs_rows,
+                                                     const int64_t* pos, int64_t total) {
   // One rounding per product and per sum, as eager PyTorch: no contraction
   // of x*c - y*s into an fma (which would drop the rounding of one product).
 #pragma clang fp contract(off)
@@ -32,7 +32,9 @@ __global__ __launch_bounds__(256) void rope16_kernel(const uint16_t* x, int64_t 
   row /= H;
   const int s = (int)(row % S);
   const int b = (int)(row / S);
-  const int64_t ps = pos ? pos[(int64_t)b * S + s] : s;
+  // position ids are clamped to the table (the host rejects out-of-range
+  // ids except while a graph is being captured, when it cannot read them)
+  const int64_t ps = pos ? min(max(pos[(int64_t)b * S + s], (int64_t)0), cs_rows - 1) : s;
   const uint16_t* xr = x + b * xsb + s * xss + h * xsh;
   uint16_t* orow = out + b * osb + s * oss + h * osh;
   const int d = c * 8, half = D / 2;
@@ -91,7 +93,7 @@ template <class S, class T>
 __global__ __launch_bounds__(256) void rope_scalar_kernel(const T* x, int64_t xsb, int64_t xss, int64_t xsh, T* out,
                                                           int64_t osb, int64_t oss, int64_t osh, int Sn, int H,
                                                           int D, const T* cosp, const T* sinp, int64_t cs,
-                                                          const int64_t* pos, int64_t total) {
+                                                          int64_t cs_rows, const int64_t* pos, int64_t total) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= total) return;
   const int half = D / 2;
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(256) void rope_scalar_kernel(const T* x, int64_t xs
   row /= H;
   const int s = (int)(row % Sn);
   const int b = (int)(row / Sn);
-  const int64_t ps = pos ? pos[(int64_t)b * Sn + s] : s;
+  const int64_t ps = pos ? min(max(pos[(int64_t)b * Sn + s], (int64_t)0), cs_rows - 1) : s;
   const T* xr = x + b * xsb + s * xss + h * xsh;
   T* orow = out + b * osb + s * oss + h * osh;
   const float a = S::ld(xr, d), bb = S::ld(xr, d + half);
@@ -154,8 +156,10 @@ extern "C" {
 
 int trinix_rope_apply(const void* x, const int64_t xs[4], void* out, const int64_t os[4], int64_t batch,
                       int64_t seqlen, int64_t nheads, int64_t head_dim, int32_t dtype, const void* cosp,
-                      const void* sinp, int64_t cs, const int64_t* position_ids, void* stream) {
+                      const void* sinp, int64_t cs, int64_t cs_rows, const int64_t* position_ids,
+                      void* stream) {
   if (!x || !out || !cosp || !sinp || !xs || !os) return TRINIX_ERR_NULL_POINTER;
+  if (cs_rows < (position_ids ? 1 : seqlen)) return TRINIX_ERR_BAD_SHAPE;
   if (batch <= 0 || seqlen <= 0 || nheads <= 0 || head_dim <= 0 || head_dim % 2) return TRINIX_ERR_BAD_SHAPE;
   if (xs[3] != 1 || os[3] != 1) return TRINIX_ERR_BAD_STRIDE;
   if (seqlen >= (1ll << 31) || batch >= (1ll << 31) || nheads >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
@@ -172,11 +176,11 @@ int trinix_rope_apply(const void* x, const int64_t xs[4], void* out, const int64
     if (dtype == TRINIX_BF16)
       hipLaunchKernelGGL(rope16_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t*)x, xs[0], xs[1], xs[2],
                          (uint16_t*)out, os[0], os[1], os[2], S, H, D, (const uint16_t*)cosp,
-                         (const uint16_t*)sinp, cs, position_ids, total);
+                         (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else if (dtype == TRINIX_F16)
       hipLaunchKernelGGL(rope16_kernel<F16>, grid, dim3(256), 0, st, (const uint16_t*)x, xs[0], xs[1], xs[2],
                          (uint16_t*)out, os[0], os[1], os[2], S, H, D, (const uint16_t*)cosp,
-                         (const uint16_t*)sinp, cs, position_ids, total);
+                         (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else
       return TRINIX_ERR_BAD_DTYPE;
   } else {
@@ -185,15 +189,15 @@ int trinix_rope_apply(const void* x, const int64_t xs[4], void* out, const int64
     if (dtype == TRINIX_BF16)
       hipLaunchKernelGGL((rope_scalar_kernel<BF16Scalar, uint16_t>), grid, dim3(256), 0, st, (const uint16_t*)x,
                          xs[0], xs[1], xs[2], (uint16_t*)out, os[0], os[1], os[2], S, H, D,
-                         (const uint16_t*)cosp, (const uint16_t*)sinp, cs, position_ids, total);
+                         (const uint16_t*)cosp, (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else if (dtype == TRINIX_F16)
       hipLaunchKernelGGL((rope_scalar_kernel<F16Scalar, uint16_t>), grid, dim3(256), 0, st, (const uint16_t*)x,
                          xs[0], xs[1], xs[2], (uint16_t*)out, os[0], os[1], os[2], S, H, D,
-                         (const uint16_t*)cosp, (const uint16_t*)sinp, cs, position_ids, total);
+                         (const uint16_t*)cosp, (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else if (dtype == TRINIX_F32)
       hipLaunchKernelGGL((rope_scalar_kernel<F32Scalar, float>), grid, dim3(256), 0, st, (const float*)x, xs[0],
                          xs[1], xs[2], (float*)out, os[0], os[1], os[2], S, H, D, (const float*)cosp,
-                         (const float*)sinp, cs, position_ids, total);
+                         (const float*)sinp, cs, cs_rows, position_ids, total);
     else
       return TRINIX_ERR_BAD_DTYPE;
   }

@@ -20,7 +20,7 @@ import torch
 
 from .. import _native as nat
 from .attention_kernel import _DTYPE_CODE, current_stream_ptr
-from .rope_kernel import _table
+from .rope_kernel import _table, check_positions
 
 QK_NORM_HEAD_DIMS = (16, 32, 64, 128, 256)
 
@@ -57,8 +57,7 @@ def qk_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, cos: Optional[
             raise ValueError("cos/sin tables narrower than head_dim/2")
         if position_ids is not None:
             pos = position_ids.to(device=x.device, dtype=torch.int64).expand(B, S).contiguous()
-            if int(pos.min()) < 0 or int(pos.max()) >= c.shape[0]:
-                raise ValueError("position_ids out of range of the cos/sin tables")
+            check_positions(pos, c.shape[0])
         elif c.shape[0] < S:
             raise ValueError("cos/sin tables shorter than the sequence")
     out = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
@@ -66,7 +65,8 @@ def qk_rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, cos: Optional[
         x.data_ptr(), (ctypes.c_int64 * 4)(*x.stride()), out.data_ptr(), (ctypes.c_int64 * 4)(*out.stride()),
         B, S, H, D, _DTYPE_CODE[x.dtype], w.data_ptr(), float(eps),
         c.data_ptr() if c is not None else None, s.data_ptr() if s is not None else None,
-        c.stride(0) if c is not None else 0, pos.data_ptr() if pos is not None else None,
+        c.stride(0) if c is not None else 0, c.shape[0] if c is not None else 0,
+        pos.data_ptr() if pos is not None else None,
         current_stream_ptr(x.device))
     nat.check(rc, "trinix_qk_norm")
     return out

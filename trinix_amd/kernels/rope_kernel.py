@@ -30,6 +30,17 @@ def _table(t: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return t
 
 
+def check_positions(pos: torch.Tensor, rows: int) -> None:
+    """Reject position ids outside the cos/sin tables (reference: indexing
+    ``cos[position_ids]`` raises).  Reading them needs a device-to-host copy,
+    which a stream under graph capture does not allow: there the check is
+    skipped and the kernels clamp ids into [0, rows) instead."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    if int(pos.min()) < 0 or int(pos.max()) >= rows:
+        raise ValueError("position_ids out of range of the cos/sin tables")
+
+
 def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                position_ids: Optional[torch.Tensor] = None,
                out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -54,8 +65,7 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     pos = None
     if position_ids is not None:
         pos = position_ids.to(device=x.device, dtype=torch.int64).expand(B, S).contiguous()
-        if int(pos.min()) < 0 or int(pos.max()) >= c.shape[0]:
-            raise ValueError("position_ids out of range of the cos/sin tables")
+        check_positions(pos, c.shape[0])
     elif c.shape[0] < S:
         raise ValueError("cos/sin tables shorter than the sequence")
     if out is None:
@@ -64,7 +74,7 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     os_ = (ctypes.c_int64 * 4)(*out.stride())
     lib = nat.load_library()
     rc = lib.trinix_rope_apply(x.data_ptr(), xs, out.data_ptr(), os_, B, S, H, D, _DTYPE_CODE[x.dtype],
-                               c.data_ptr(), s.data_ptr(), c.stride(0),
+                               c.data_ptr(), s.data_ptr(), c.stride(0), c.shape[0],
                                pos.data_ptr() if pos is not None else None,
                                current_stream_ptr(x.device))
     nat.check(rc, "trinix_rope_apply")
