@@ -205,3 +205,40 @@ def test_qk_norm_rejects_before_launch(lib):
                               None, None) == nat.TRINIX_ERR_BAD_SHAPE
     assert lib.trinix_rope_apply(4096, st, 4096, st, 1, 64, 8, 128, nat.TRINIX_BF16, 4096, 4096, 64, 63,
                                  None, None) == nat.TRINIX_ERR_BAD_SHAPE
+
+
+def test_splitkv_plan_invariants_random(lib):
+    """For random decode shapes the plan's chunks tile the visible keys:
+    chunk a multiple of 64 and >= 64, ceil(span / chunk) chunks, workspace =
+    rows * chunks * (D + 1) * 4 bytes when there is more than one chunk."""
+    import random
+
+    r = random.Random(7)
+    for _ in range(300):
+        Hkv = r.choice([1, 2, 4, 8])
+        kw = dict(batch=r.randint(1, 300), seqlen_q=r.randint(1, 16), seqlen_k=r.randint(1, 100000),
+                  nheads_kv=Hkv, nheads_q=Hkv * r.choice([1, 2, 4, 8]), head_dim=r.choice([64, 128]))
+        if r.random() < 0.3:
+            kw["causal"] = 1
+        if r.random() < 0.3:
+            kw.update(has_window=1, window_left=r.randint(-50, 5000), window_right=r.randint(-50, 5000))
+        ns, wb = _plan(lib, **kw)
+        Sq, Sk = kw["seqlen_q"], kw["seqlen_k"]
+        lo, hi = 0, Sk - 1
+        if kw.get("causal"):
+            hi = min(hi, Sq - 1)
+        if kw.get("has_window"):
+            lo = max(lo, -kw["window_left"])
+            hi = min(hi, Sq - 1 + kw["window_right"])
+        lo, khi = min(lo, Sk), max(0, min(Sk, hi + 1))
+        span = khi - lo
+        if span <= 0:
+            assert ns == 0
+            continue
+        assert ns >= 1
+        rows = kw["nheads_q"] // Hkv * Sq
+        items = kw["batch"] * Hkv * ((rows + 15) // 16)
+        chunk = -(-span // ns)
+        assert ns == 1 or (ns - 1) * ((chunk + 63) // 64 * 64) < span
+        assert items * ns < 2 ** 31
+        assert wb == (0 if ns == 1 else kw["batch"] * Hkv * rows * ns * (kw["head_dim"] + 1) * 4)
