@@ -40,6 +40,9 @@ def parse():
     ap.add_argument("--cpu-sample-heads", type=int, default=32,
                     help="query heads of batch 0 timed on the CPU oracle")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="time the workload only: no MALL-flushed, forward+backward, decode or layer fields "
+                         "(for profiler runs)")
     ap.add_argument("--all", action="store_true", help="also time every other workload (extra field)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (scale factor of the HBM byte counters)")
@@ -340,7 +343,7 @@ def main():
 
     w = WORKLOADS[args.workload]
     dname = DTYPE_NAME[str(w.dtype)]
-    inp, fl, ms, kms, cold_ms = measure(w, args, torch, cold=True)
+    inp, fl, ms, kms, cold_ms = measure(w, args, torch, cold=not args.no_extra)
     value = fl / (ms * 1e-3) / 1e12
     k_tflops = fl / (kms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[dname]
@@ -378,15 +381,16 @@ def main():
             "algorithmic_bytes": algo_bytes(w),
         },
         "native_library": str(_native.LIB_PATH) if _native.library_loaded() else None,
-        # the same step with q/k/v evicted from the 256 MB MALL before each call
-        "cold_mall": {"ms_per_step": round(cold_ms, 4), "tflops": round(fl / cold_ms / 1e9, 2)},
     }
-    if dname in ("bf16", "fp16") and not w.alibi and not w.block_mask:
+    if cold_ms is not None:
+        # the same step with q/k/v evicted from the 256 MB MALL before each call
+        rec["cold_mall"] = {"ms_per_step": round(cold_ms, 4), "tflops": round(fl / cold_ms / 1e9, 2)}
+    if dname in ("bf16", "fp16") and not w.alibi and not w.block_mask and not args.no_extra:
         # forward + backward (3.5x the forward FLOP by the usual convention)
         fb = fwd_bwd_ms(w, inp, torch)
         rec["fwd_bwd"] = {"ms": round(fb, 4), "tflops": round(3.5 * fl / fb / 1e9, 2),
                           "bwd_ms": round(fb - ms, 4), "bwd_tflops": round(2.5 * fl / (fb - ms) / 1e9, 2)}
-    if dname in ("bf16", "fp16"):
+    if dname in ("bf16", "fp16") and not args.no_extra:
         del inp
         torch.cuda.empty_cache()
         rec["decode"] = decode_measure(torch)
