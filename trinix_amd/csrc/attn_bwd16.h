@@ -135,7 +135,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
 
   // ---- tile copies: Q and dO rows (16-byte units, swizzled), lse and delta
   auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
-  auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_k<D>(ld_row(l)); };
+  auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_kt<D>(ld_row(l)); };
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
   auto load_rows = [&](const uint16_t* base, int64_t ss, uint16_t* lds_tile, int i0) __attribute__((always_inline)) {
     const uint64_t gb = uniform_ptr((const char*)base + (int64_t)i0 * ss * 2);
@@ -163,10 +163,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
     if (wave == 1) load_vec(p.delta + vo, SL ? lds_d1 : lds_d0, i0);
   };
 
-  // ---- LDS operand reads of a Q / dO tile (rows swizzled with swz_k)
+  // ---- LDS operand reads of a Q / dO tile (rows swizzled with swz_kt)
   // Row read (A operand of S / dP): query row qrow, head_dim chunk ds.
   auto rowread = [&](const uint16_t* tile, int qrow, int ds) __attribute__((always_inline)) {
-    const int unit = (ds * 2 + g) ^ swz_k<D>(qrow);
+    const int unit = (ds * 2 + g) ^ swz_kt<D>(qrow);
     return *(const u32x4_t*)(tile + qrow * D + unit * 8);
   };
   // Transpose read (A operand of dV^T / dK^T): head_dim rows db*32 + l%32,
@@ -179,9 +179,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
     const int row0 = st * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
     const int row1 = row0 + 8;
     const s16x4_t lo4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_k<D>(row0)) * 8 + half));
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_kt<D>(row0)) * 8 + half));
     const s16x4_t hi4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_k<D>(row1)) * 8 + half));
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_kt<D>(row1)) * 8 + half));
     const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
@@ -375,7 +375,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
   const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
   auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
-  auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_k<D>(ld_row(l)); };
+  auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_kt<D>(ld_row(l)); };
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
   auto load_rows = [&](const uint16_t* base, int64_t ss, uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
     const int n0 = tile * BN;
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
     }
   };
   auto rowread = [&](const uint16_t* tile, int krow, int ds) __attribute__((always_inline)) {
-    const int unit = (ds * 2 + g) ^ swz_k<D>(krow);
+    const int unit = (ds * 2 + g) ^ swz_kt<D>(krow);
     return *(const u32x4_t*)(tile + krow * D + unit * 8);
   };
   const int tr_G = lane >> 4, tr_s = lane & 15, tr_g = tr_G >> 1, tr_dh = tr_G & 1;
@@ -400,9 +400,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
     const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
     const int row1 = row0 + 8;
     const s16x4_t lo4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_k<D>(row0)) * 8 + half));
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_kt<D>(row0)) * 8 + half));
     const s16x4_t hi4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_k<D>(row1)) * 8 + half));
+        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_kt<D>(row1)) * 8 + half));
     const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
