@@ -187,9 +187,13 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
   };
 
   // ---- one 32-query sub-tile against this wavefront's 32 keys
-  auto subtile = [&](auto pred_c, const uint16_t* qt_lds, const uint16_t* ot_lds, const float* l_lds,
+  // `edge`: the sub-tile has pairs outside the band / past Sq or Sk.  It is a
+  // runtime flag, and only the masking of the scores branches on it: with the
+  // whole sub-tile instantiated twice, the two copies of the dK/dV MFMAs left
+  // the 128 accumulator registers in different places and every sub-tile
+  // paid 128 register moves at the join.
+  auto subtile = [&](bool edge, const uint16_t* qt_lds, const uint16_t* ot_lds, const float* l_lds,
                      const float* d_lds, int st, int i0, int hq, float slope_l2, int mcode) __attribute__((always_inline)) {
-    constexpr bool PRED = decltype(pred_c)::value;
     f32x16_t s = {}, dp = {};
 #pragma unroll
     for (int ds = 0; ds < DS; ++ds) s = E::mfma(rowread(qt_lds, st * 32 + r, ds), kr[ds], s);
@@ -203,6 +207,23 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
         mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)jc * p.mk_sj) * esz;
       }
     }
+    float x[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+      x[v] = s[v] * c;
+      if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - j);
+      if constexpr (MASK) {
+        if (mcode > 0 && i < p.Sq) x[v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)i * p.mk_si) * kLog2e;
+      }
+    }
+    if (edge) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+        x[v] = (band.ok(i, j) && i < p.Sq && j < p.Sk) ? x[v] : -INFINITY;
+      }
+    }
     float pv[16], dz[16];
 #pragma unroll
     for (int vq = 0; vq < 4; ++vq) {
@@ -211,14 +232,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int v = vq * 4 + e;
-        const int i = i0 + st * 32 + vq * 8 + g * 4 + e;
-        float x = s[v] * c;
-        if constexpr (ALIBI) x += slope_l2 * (float)abs(i - j);
-        if constexpr (MASK) {
-          if (mcode > 0 && i < p.Sq) x += load_mask_elem(mrow, p.mask_dtype, (int64_t)i * p.mk_si) * kLog2e;
-        }
-        if constexpr (PRED) x = (band.ok(i, j) && i < p.Sq && j < p.Sk) ? x : -INFINITY;
-        const float pe = __builtin_amdgcn_exp2f(x - l4[e] * kLog2e);
+        const float pe = __builtin_amdgcn_exp2f(x[v] - l4[e] * kLog2e);
         pv[v] = pe;
         dz[v] = pe * (dp[v] - d4[e]);
       }
@@ -274,8 +288,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
           }
         }
         const bool full = ia + 31 < p.Sq && j0 + 31 < p.Sk && jb - ia <= band.dhi && j0 - ib >= band.dlo;
-        if (full) subtile(std::false_type{}, qt_lds, ot_lds, l_lds, d_lds, st, i0, hq, slope_l2, mcode);
-        else subtile(std::true_type{}, qt_lds, ot_lds, l_lds, d_lds, st, i0, hq, slope_l2, mcode);
+        subtile(!full, qt_lds, ot_lds, l_lds, d_lds, st, i0, hq, slope_l2, mcode);
       }
     };
     int qt = qt_lo;
@@ -407,8 +420,10 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
 
-  auto tile_body = [&](auto pred_c, const uint16_t* kt, const uint16_t* vt, int t) __attribute__((always_inline)) {
-    constexpr bool PRED = decltype(pred_c)::value;
+  // `edge` is a runtime flag and only the masking of the scores branches on
+  // it (two instantiated copies of the dQ MFMAs cost 64 accumulator moves at
+  // every join).
+  auto tile_body = [&](bool edge, const uint16_t* kt, const uint16_t* vt, int t) __attribute__((always_inline)) {
     const int n0 = t * BN;
     int mcode = 1;
     if constexpr (MASK) {
@@ -427,20 +442,34 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) dp[nb] = E::mfma(rowread(vt, nb * 32 + r, ds), dor[ds], dp[nb]);
     }
+    float x[NB][16];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+        x[nb][v] = s[nb][v] * c;
+        if constexpr (ALIBI) x[nb][v] += slope_l2 * (float)abs(i - jj);
+        if constexpr (MASK) {
+          if (mcode > 0 && jj < p.Sk) x[nb][v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
+        }
+      }
+    if (edge) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          x[nb][v] = (band.ok(i, jj) && jj < p.Sk && i < p.Sq) ? x[nb][v] : -INFINITY;
+        }
+    }
     u32x4_t zb[NB][2];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       float z[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        float x = s[nb][v] * c;
-        if constexpr (ALIBI) x += slope_l2 * (float)abs(i - jj);
-        if constexpr (MASK) {
-          if (mcode > 0 && jj < p.Sk) x += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
-        }
-        if constexpr (PRED) x = (band.ok(i, jj) && jj < p.Sk && i < p.Sq) ? x : -INFINITY;
-        const float pe = __builtin_amdgcn_exp2f(x - lse2);
+        const float pe = __builtin_amdgcn_exp2f(x[nb][v] - lse2);
         z[v] = pe * (dp[nb][v] - dlt);
       }
 #pragma unroll
@@ -476,8 +505,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
     const int nl = min(n0 + BN, p.Sk) - 1;
     if (!wave_live || n0 - iwl > band.dhi || nl - iw0 < band.dlo) return;  // no allowed pair
     const bool full = iw0 + 31 < p.Sq && n0 + BN <= p.Sk && nl - iw0 <= band.dhi && n0 - iwl >= band.dlo;
-    if (full) tile_body(std::false_type{}, kt, vt, t);
-    else tile_body(std::true_type{}, kt, vt, t);
+    tile_body(!full, kt, vt, t);
   };
   int t = t_lo;
   for (; t + 1 < t_hi; t += 2) {
