@@ -70,6 +70,24 @@ struct Band {
   __device__ bool ok(int i, int j) const { return j - i >= dlo && j - i <= dhi; }
 };
 
+// Allowed range [lo, lo + span] of one index as an unsigned interval test:
+// (uint32_t)(x - lo) <= span is one subtract and one compare per element (an
+// empty range gets lo = INT_MAX, which no x in [0, 2^30) passes).
+struct Span {
+  int lo;
+  uint32_t span;
+  __device__ Span(int64_t a, int64_t b) {
+    if (b < a) {
+      lo = INT_MAX;
+      span = 0u;
+    } else {
+      lo = (int)a;
+      span = (uint32_t)(b - a);
+    }
+  }
+  __device__ bool ok(int x) const { return (uint32_t)(x - lo) <= span; }
+};
+
 // ---------------------------------------------------------------------------
 // dK, dV.  Lane l of wavefront w owns key j = kb0 + 32w + l%32.  Per 32-query
 // sub-tile: S = Q K^T and dP = dO V^T with the query rows on the MFMA rows
@@ -108,6 +126,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
   const int j = j0 + r;
   const int jc = min(j, p.Sk - 1);
   const Band band(p);
+  // queries this lane's key may see: j - dhi <= i <= j - dlo, 0 <= i < Sq (none if j >= Sk)
+  const Span qspan = j < p.Sk ? Span(max((int64_t)0, (int64_t)j - band.dhi), min((int64_t)p.Sq - 1, (int64_t)j - band.dlo))
+                              : Span(1, 0);
   const float c = p.scale_log2;
 
   // this lane's K and V rows (B operands of S and dP)
@@ -221,7 +242,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        x[v] = (band.ok(i, j) && i < p.Sq && j < p.Sk) ? x[v] : -INFINITY;
+        x[v] = qspan.ok(i) ? x[v] : -INFINITY;
       }
     }
     float pv[16], dz[16];
@@ -352,6 +373,9 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
   const int i = iw0 + r;
   const int ic = min(i, p.Sq - 1);
   const Band band(p);
+  // keys this lane's row may see: i + dlo <= j <= i + dhi, 0 <= j < Sk (none if i >= Sq)
+  const Span kspan = i < p.Sq ? Span(max((int64_t)0, (int64_t)i + band.dlo), min((int64_t)p.Sk - 1, (int64_t)i + band.dhi))
+                              : Span(1, 0);
   const float c = p.scale_log2;
 
   u32x4_t qr[DS], dor[DS];
@@ -460,7 +484,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-          x[nb][v] = (band.ok(i, jj) && jj < p.Sk && i < p.Sq) ? x[nb][v] : -INFINITY;
+          x[nb][v] = kspan.ok(jj) ? x[nb][v] : -INFINITY;
         }
     }
     u32x4_t zb[NB][2];
