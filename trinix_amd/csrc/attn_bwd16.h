@@ -88,6 +88,45 @@ struct Span {
   __device__ bool ok(int x) const { return (uint32_t)(x - lo) <= span; }
 };
 
+// LDS operand reads of a row-major, D-wide 16-bit tile swizzled with
+// swz_kt.  The per-lane parts of the addresses are computed once; each read
+// adds its row-block offset as an immediate.  Adding a multiple of 16 rows
+// leaves swz_kt unchanged (it depends on row bits 0-3), so:
+//  * row read (A operand, row blk*32 + l%32, head_dim chunk ds):
+//      byte offset blk*32*D*2 + (row_lane ^ 32*ds), as
+//      16*((2ds + g) ^ swz) = 32*ds ^ 16*(g ^ swz) and the row part r*D*2
+//      has no bits below bit 7;
+//  * transpose read (A operand over 8 rows: rows t and t+8 of k-step kk of
+//      sub-tile st, head_dim block db): (st*32 + kk*16)*D*2 + tr0[db] / tr1[db].
+template <int D>
+struct TileReader {
+  static constexpr int DB = D / 32;
+  uint32_t row_lane;
+  uint32_t tr0[DB], tr1[DB];
+  __device__ explicit TileReader(int lane) {
+    const int r = lane & 31, g = lane >> 5;
+    row_lane = (uint32_t)(r * D * 2 + 16 * (g ^ swz_kt<D>(r)));
+    const int tr_G = lane >> 4, tr_s = lane & 15, tr_g = tr_G >> 1, tr_dh = tr_G & 1;
+    const int row0 = tr_g * 4 + (tr_s >> 2), row1 = row0 + 8;
+    const int c = tr_dh * 2 + ((tr_s & 3) >> 1), half = (tr_s & 1) * 4;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      tr0[db] = (uint32_t)((row0 * D + (((db * 4) | c) ^ swz_kt<D>(row0)) * 8 + half) * 2);
+      tr1[db] = (uint32_t)((row1 * D + (((db * 4) | c) ^ swz_kt<D>(row1)) * 8 + half) * 2);
+    }
+  }
+  __device__ u32x4_t row(const uint16_t* tile, int blk, int ds) const {
+    return *(const u32x4_t*)((const char*)tile + blk * 32 * D * 2 + (row_lane ^ (uint32_t)(ds << 5)));
+  }
+  __device__ u32x4_t tr(const uint16_t* tile, int st, int db, int kk) const {
+    const char* base = (const char*)tile + (st * 32 + kk * 16) * D * 2;
+    const s16x4_t lo4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(base + tr0[db]));
+    const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(base + tr1[db]));
+    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
+    return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
+  }
+};
+
 // ---------------------------------------------------------------------------
 // dK, dV.  Lane l of wavefront w owns key j = kb0 + 32w + l%32.  Per 32-query
 // sub-tile: S = Q K^T and dP = dO V^T with the query rows on the MFMA rows
@@ -345,7 +384,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
 // dQ^T += K^T dZ^T with K^T from LDS transpose reads.
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
   constexpr int NW = 4, BM = NW * 32, BN = 64;
   constexpr int DS = D / 16, DB = D / 32, NB = BN / 32, UPR = D / 8;
   constexpr int LPW = BN * UPR / (64 * NW);
@@ -426,23 +465,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
                 __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
     }
   };
-  auto rowread = [&](const uint16_t* tile, int krow, int ds) __attribute__((always_inline)) {
-    const int unit = (ds * 2 + g) ^ swz_kt<D>(krow);
-    return *(const u32x4_t*)(tile + krow * D + unit * 8);
-  };
-  const int tr_G = lane >> 4, tr_s = lane & 15, tr_g = tr_G >> 1, tr_dh = tr_G & 1;
-  auto trread = [&](const uint16_t* tile, int nb, int db, int kk) __attribute__((always_inline)) {
-    const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);
-    const int half = (tr_s & 1) * 4;
-    const int row0 = nb * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
-    const int row1 = row0 + 8;
-    const s16x4_t lo4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_kt<D>(row0)) * 8 + half));
-    const s16x4_t hi4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_kt<D>(row1)) * 8 + half));
-    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
-    return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
-  };
+  const TileReader<D> rd(lane);
 
   // `edge` is a runtime flag and only the masking of the scores branches on
   // it (two instantiated copies of the dQ MFMAs cost 64 accumulator moves at
@@ -457,56 +480,79 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq(const BwdParams p) {
         mcode = code == 0 ? 0 : 1;
       }
     }
-    f32x16_t s[NB], dp[NB];
+    // One 32-key half at a time (S, dP, dZ, then its dQ products): only one
+    // pair of 32x32 score tiles is live, and with the operand reads pinned
+    // PF MFMAs ahead (sched_group_barrier: 0x100 LDS read, 0x008 MFMA) the
+    // kernel fits the 256 registers of two wavefronts per SIMD.
+    constexpr int PF = ALIBI ? 2 : 4;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      s[nb] = dp[nb] = (f32x16_t){};
+      f32x16_t s = (f32x16_t){}, dp = (f32x16_t){};
+      {
+        auto kvread = [&](int k) __attribute__((always_inline)) {
+          return k < DS ? rd.row(kt, nb, k) : rd.row(vt, nb, k - DS);
+        };
+        u32x4_t f[2 * DS];
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) s[nb] = E::mfma(rowread(kt, nb * 32 + r, ds), qr[ds], s[nb]);
+        for (int k = 0; k < PF; ++k) f[k] = kvread(k);
 #pragma unroll
-      for (int ds = 0; ds < DS; ++ds) dp[nb] = E::mfma(rowread(vt, nb * 32 + r, ds), dor[ds], dp[nb]);
-    }
-    float x[NB][16];
+        for (int k = 0; k < 2 * DS; ++k) {
+          if (k + PF < 2 * DS) f[k + PF] = kvread(k + PF);
+          if (k < DS) s = E::mfma(f[k], qr[k], s);
+          else dp = E::mfma(f[k], dor[k - DS], dp);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+        for (int k = 0; k < 2 * DS; ++k) {
+          if (k + PF < 2 * DS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+      }
+      float x[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        x[nb][v] = s[nb][v] * c;
-        if constexpr (ALIBI) x[nb][v] += slope_l2 * (float)abs(i - jj);
+        x[v] = s[v] * c;
+        if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - jj);
         if constexpr (MASK) {
-          if (mcode > 0 && jj < p.Sk) x[nb][v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
+          if (mcode > 0 && jj < p.Sk) x[v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
         }
       }
-    if (edge) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+      if (edge) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-          x[nb][v] = kspan.ok(jj) ? x[nb][v] : -INFINITY;
+          x[v] = kspan.ok(jj) ? x[v] : -INFINITY;
         }
-    }
-    u32x4_t zb[NB][2];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      float z[16];
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float pe = __builtin_amdgcn_exp2f(x[nb][v] - lse2);
-        z[v] = pe * (dp[nb][v] - dlt);
       }
+      u32x4_t zb[2];
+      {
+        float z[16];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        zb[nb][kk] = (u32x4_t){E::pack(z[kk * 8 + 0], z[kk * 8 + 1]), E::pack(z[kk * 8 + 2], z[kk * 8 + 3]),
-                               E::pack(z[kk * 8 + 4], z[kk * 8 + 5]), E::pack(z[kk * 8 + 6], z[kk * 8 + 7])};
+        for (int v = 0; v < 16; ++v) z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dp[v] - dlt);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          zb[kk] = (u32x4_t){E::pack(z[kk * 8 + 0], z[kk * 8 + 1]), E::pack(z[kk * 8 + 2], z[kk * 8 + 3]),
+                             E::pack(z[kk * 8 + 4], z[kk * 8 + 5]), E::pack(z[kk * 8 + 6], z[kk * 8 + 7])};
+      }
+      {
+        constexpr int NM = DB * 2;
+        u32x4_t f[NM];
+#pragma unroll
+        for (int m = 0; m < PF; ++m) f[m] = rd.tr(kt, nb, m / 2, m % 2);
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          if (m + PF < NM) f[m + PF] = rd.tr(kt, nb, (m + PF) / 2, (m + PF) % 2);
+          acc[m / 2] = E::mfma(f[m], zb[m % 2], acc[m / 2]);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * PF, 0);
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+          if (m + PF < NM) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+      }
     }
-#pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) acc[db] = E::mfma(trread(kt, nb, db, kk), zb[nb][kk], acc[db]);
   };
 
   if (t_lo < t_hi) {
