@@ -114,7 +114,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   int t_fhi = fhi > 0 ? (int)(fhi / BN) : 0;
   t_flo = min(max(t_flo, t_lo), t_hi);
   t_fhi = min(max(t_fhi, t_flo), t_hi);
-  if (!(p.scale_log2 > 0.f)) t_flo = t_fhi = t_hi;  // raw-max trick needs scale > 0
+  // Scores in log2 units: x = q.k * c (+ bias).  ALiBi with scale 0 drops the
+  // q.k term (q operand zeroed) and uses c = 1, so that its bias can ride in
+  // the score accumulator (seed_scores) as for any other scale.
+  const bool alibi_zero_scale = ALIBI && p.scale_log2 == 0.f;
+  const float c = alibi_zero_scale ? 1.f : p.scale_log2;
+  if (!(c > 0.f)) t_flo = t_fhi = t_hi;  // raw-max trick needs scale > 0
 
   // Q row in registers: qr[ds] = q[i][ds*16 + g*8 .. +8].
   u32x4_t qr[DS];
@@ -152,13 +157,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
         qr[ds + DS / 2] = x2;
       }
     }
+    if (alibi_zero_scale)
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) qr[ds] = (u32x4_t){};
   }
 
   f32x16_t acc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) acc[db] = (f32x16_t){};
   float m_run = -INFINITY, l_run = 0.f;
-  const float c = p.scale_log2;
   // Allowed keys of this row: jlo <= j <= jhi (empty if jlo > jhi), from
   // j < Sk, causal j <= i and window -wl <= j - i <= wr (clamped to int32).
   int jlo = 0, jhi = p.Sk - 1;
@@ -171,6 +178,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   if (jhi < jlo) jlo = INT_MAX;  // no allowed key: (j - jlo) wraps past jspan for every j
   float slope_l2 = 0.f;
   if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
+  // ALiBi is folded into the score accumulator: S^T starts at bias / c
+  // instead of 0, so s * c = q.k * c + bias and the softmax of a full tile is
+  // the plain one (raw max, one FMA before the exp).
+  const float alibi_seed_mul = ALIBI ? slope_l2 / c : 0.f;
   const char* mrow = nullptr;
   if constexpr (MASK) {
     const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
@@ -226,18 +237,55 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
 
   // ---- per-tile pieces ---------------------------------------------------
-  auto mask_code = [&](int n0) __attribute__((always_inline)) -> int {
-    if (!p.bmap) return 1;
-    const uint8_t* bm = p.bmap + b * p.bm_sb + hq * p.bm_sh + (int64_t)(iw0 / 32) * p.bm_cols;
+  // Block-map codes of this wavefront's 32-row block (one per 64-key column)
+  // are fetched 64 columns at a time into one register, lane l holding column
+  // bm_c0 + l, ahead of the tile wait that covers their latency; a tile reads
+  // its codes with readlane.  (A load at the tile's use would wait for the
+  // next tile's K/V loads as well: both count on the same vmcnt.)  At D = 256
+  // (one wavefront per SIMD, every register in use) the codes and their
+  // fetch would push the mask kernels into spilling, so there every tile
+  // reads the mask per element instead.
+  constexpr int NCB = BN / 64;  // block-map columns per tile
+  const uint8_t* bm_row = nullptr;
+  if constexpr (MASK && D <= 128)
+    if (p.bmap && wave_live) bm_row = p.bmap + b * p.bm_sb + hq * p.bm_sh + (int64_t)(iw0 / 32) * p.bm_cols;
+  uint32_t bm_codes = 0;
+  int bm_c0 = 0;
+  auto bm_fetch = [&](int col0) __attribute__((always_inline)) {
+    bm_c0 = col0;
+    const int col = col0 + lane;
+    bm_codes = col < p.bm_cols ? bm_row[col] : 0u;
+  };
+  // -1: every block of the tile is -inf (skip); 0: all zero (no mask term);
+  // 1: read the mask per element.
+  auto mask_code = [&](int t) __attribute__((always_inline)) -> int {
+    if (!bm_row) return 1;
     bool all_skip = true, any_other = false;
 #pragma unroll
-    for (int cb = 0; cb < BN / 64; ++cb) {
-      if (n0 + cb * 64 >= p.Sk) break;  // past the last block-map column
-      const uint8_t code = bm[n0 / 64 + cb];
+    for (int cb = 0; cb < NCB; ++cb) {
+      const int col = t * NCB + cb;
+      if (col >= p.bm_cols) break;  // past the last block-map column
+      const uint32_t code = (uint32_t)__builtin_amdgcn_readlane((int)bm_codes, col - bm_c0);
       all_skip = all_skip && code == 2;
       any_other = any_other || code != 0;
     }
     return all_skip ? -1 : (any_other ? 1 : 0);
+  };
+  // Seed of the S^T accumulators: bias / c of ALiBi (element (nb, vq*4 + e)
+  // is key n0 + nb*32 + vq*8 + 4g + e of row i), else 0.
+  auto seed_scores = [&](int n0, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
+    if constexpr (ALIBI) {
+      const float fi = (float)(i - n0 - 4 * g);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = fabsf(fi - (float)(nb * 32 + vq * 8 + e)) * alibi_seed_mul;
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) s[nb] = (f32x16_t){};
+    }
   };
 
   // S^T = K Q^T for one tile (keys nb*32 + MFMA row, queries on columns).
@@ -246,7 +294,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   constexpr int NQK = NB * DS;
   // mask kernels (and D = 256, with 192 registers of Q and O) hold more live
   // values: shorter read-ahead
-  constexpr int KPF = D == 256 ? 2 : (MASK ? 3 : 6);
+  constexpr int KPF = D == 256 ? 2 : (MASK && D > 64 ? 3 : 6);
   // Byte offset of K fragment (nb, ds) of this lane in a K tile: row
   // nb*32 + r, unit (2ds + g) ^ swz_k(r) (the swizzle depends only on r).  As
   // 16*((2ds) ^ (g ^ swz)) = 32*ds ^ 16*(g ^ swz) and the row offset has no
@@ -254,7 +302,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // are loop-invariant and live in registers; each read uses one directly,
   // with nb's row offset in the instruction's immediate.
   const uint32_t k_lane = (uint32_t)(r * D * 2 + 16 * (g ^ swz_k<D>(r)));
-  auto qk = [&](const uint16_t* kt, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
+  auto qk = [&](const uint16_t* kt, int n0, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
     auto kread = [&](int k) __attribute__((always_inline)) {
       const int nb = k / DS, ds = k % DS;
       const uint32_t off = k_lane ^ (uint32_t)(ds << 5);
@@ -263,8 +311,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     u32x4_t kf[NQK];
 #pragma unroll
     for (int k = 0; k < KPF; ++k) kf[k] = kread(k);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) s[nb] = (f32x16_t){};
+    seed_scores(n0, s);
 #pragma unroll
     for (int k = 0; k < NQK; ++k) {
       if (k + KPF < NQK) kf[k + KPF] = kread(k + KPF);
@@ -309,7 +356,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
   constexpr int NPV = DB * NB * 2;
-  constexpr int VPF = D == 256 ? 2 : (MASK ? 2 : 4);
+  constexpr int VPF = D == 256 ? 2 : (MASK && D > 64 ? 2 : 4);
   // vpre: the first VPF fragments, read ahead (before the softmax) by the caller.
   auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2], const u32x4_t(&vpre)[VPF]) __attribute__((always_inline)) {
     u32x4_t vf[NPV];
@@ -332,13 +379,15 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
 
   // Softmax update of one tile; writes P^T packed as the PV B operand.
-  // GENERIC (edge tile, ALiBi or mask): x = s*c + bias (or -inf where not
-  // allowed); plain full tiles keep raw scores, take the max of the raw
-  // scores (c > 0) and fold the scale into one FMA before the exp.
-  auto softmax = [&](auto pred_c, f32x16_t(&s)[NB], int n0, int mcode, u32x4_t(&pb)[NB][2])
+  // GENERIC (edge tile, or a tile that reads the mask): x = s*c + mask (or
+  // -inf where not allowed); plain full tiles keep raw scores, take the max
+  // of the raw scores (c > 0) and fold the scale into one FMA before the exp.
+  // ALiBi is in the scores already (seed_scores).
+  auto softmax = [&](auto pred_c, auto mask_c, f32x16_t(&s)[NB], int n0, int mcode, u32x4_t(&pb)[NB][2])
                      __attribute__((always_inline)) {
     constexpr bool PRED = decltype(pred_c)::value;
-    constexpr bool GENERIC = PRED || ALIBI || MASK;
+    constexpr bool MASKC = decltype(mask_c)::value;
+    constexpr bool GENERIC = PRED || MASKC;
     float mx = -INFINITY;
     if constexpr (GENERIC) {
 #pragma unroll
@@ -347,19 +396,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
         for (int vq = 0; vq < 4; ++vq) {
           const int j0 = n0 + nb * 32 + vq * 8 + g * 4;
           float mv[4] = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (MASK) {
-            if (mcode > 0) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                if (j0 + e < p.Sk) mv[e] = load_mask_elem(mrow, p.mask_dtype, (int64_t)(j0 + e) * p.mk_sj);
-            }
+          if constexpr (MASKC) {
+            if (mcode > 0) load_mask4(mrow, p.mask_dtype, j0, p.mk_sj, p.Sk - 1, mv);
           }
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int j = j0 + e;
             float x = s[nb][vq * 4 + e] * c;
-            if constexpr (ALIBI) x += slope_l2 * (float)abs(i - j);
-            if constexpr (MASK) x += mv[e] * kLog2e;
+            if constexpr (MASKC) x += mv[e] * kLog2e;
             if constexpr (PRED) x = (uint32_t)(j - jlo) <= jspan ? x : -INFINITY;
             s[nb][vq * 4 + e] = x;
             mx = fmaxf(mx, x);
@@ -454,6 +498,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
       if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
       else return std::integral_constant<int, 1 - decltype(slot)::value>{};
     }();
+    if constexpr (MASK && D <= 128)
+      if (bm_row && (t + 1) * NCB - bm_c0 > 64) bm_fetch(t * NCB);  // next 64 columns, before the wait
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
     __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
     if (t + 1 < t_hi) {
@@ -462,25 +508,34 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     }
     if (tile_live(t)) {
       const int n0 = t * BN;
-      int mcode = 1;
-      if constexpr (MASK) mcode = mask_code(n0);
+      // MFMA sections at raised priority: the other wavefront on this SIMD
+      // fills the MFMA pipe gaps with its softmax VALU work.
+      const int mcode = MASK ? mask_code(t) : 0;
       if (mcode >= 0) {
-        // MFMA sections at raised priority: the other wavefront on this SIMD
-        // fills the MFMA pipe gaps with its softmax VALU work.
         f32x16_t sc[NB];
         u32x4_t vpre[VPF];
         __builtin_amdgcn_s_setprio(1);
-        qk(kbuf(slot), sc);
+        qk(kbuf(slot), n0, sc);
         vprefetch(vbuf(slot), vpre);  // V operand reads in flight during the softmax
         __builtin_amdgcn_s_setprio(0);
         u32x4_t pb[NB][2];
-        softmax(pred_c, sc, n0, mcode, pb);
+        // At D = 64 (registers to spare) a full tile whose mask blocks are
+        // all zero runs the plain softmax; larger head dims keep one softmax
+        // body, as two would spill.
+        if constexpr (MASK && D <= 64 && !decltype(pred_c)::value) {
+          if (mcode == 0) softmax(pred_c, std::false_type{}, sc, n0, mcode, pb);
+          else softmax(pred_c, std::true_type{}, sc, n0, mcode, pb);
+        } else {
+          softmax(pred_c, std::bool_constant<MASK>{}, sc, n0, mcode, pb);
+        }
         __builtin_amdgcn_s_setprio(1);
         pv(vbuf(slot), pb, vpre);
         __builtin_amdgcn_s_setprio(0);
       }
     }
   };
+  if constexpr (MASK && D <= 128)
+    if (bm_row) bm_fetch(t_lo * NCB);
   if (t_lo < t_hi) {
     load_k(kbuf(std::integral_constant<int, 0>{}), t_lo);
     load_v(vbuf(std::integral_constant<int, 0>{}), t_lo);

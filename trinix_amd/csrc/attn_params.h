@@ -54,6 +54,33 @@ __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx)
   }
 }
 
+// Mask values of keys j0..j0+3 (element stride sj) of one row: one
+// wave-uniform dtype switch for the four loads, keys past jmax read key jmax
+// (their scores are masked anyway), so the loads carry no branches.
+__device__ inline void load_mask4(const void* base, int dtype, int j0, int64_t sj, int jmax, float (&mv)[4]) {
+  int64_t idx[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) idx[e] = (int64_t)min(j0 + e, jmax) * sj;
+  switch (dtype) {
+    case TRINIX_F32:
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mv[e] = ((const float*)base)[idx[e]];
+      break;
+    case TRINIX_F16:
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mv[e] = (float)((const _Float16*)base)[idx[e]];
+      break;
+    case TRINIX_BF16:
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mv[e] = __uint_as_float(((uint32_t)((const uint16_t*)base)[idx[e]]) << 16);
+      break;
+    default:
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mv[e] = (float)((const uint8_t*)base)[idx[e]];
+      break;
+  }
+}
+
 // Dropout on keys j0..j0+3 of row i: p <- keep ? p/(1-p) : 0.  Counter
 // (j0/4, i, b*H+h, offset_lo), key (seed_lo ^ offset_hi, seed_hi); word e
 // decides key j0+e.
