@@ -77,15 +77,32 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane & 31, g = lane >> 5;
 
-  // work item: (b, kv-head, m-block, q-head within the group), the q-heads
-  // sharing a KV head adjacent so they run on one XCD and share its L2.
-  int w = xcd_remap(blockIdx.x, p.total_work);
-  const int gq = w % p.G;
-  w /= p.G;
-  const int mi = w % p.num_mblk;
-  w /= p.num_mblk;
-  const int hkv = w % p.Hkv;
-  const int b = w / p.Hkv;
+  // work item: (b, kv-head, m-block, q-head within the group).  Each XCD owns
+  // whole KV-head groups, so the q-heads sharing a KV head run on one XCD and
+  // share its L2.  Causal row blocks are dispatched longest first across all
+  // the head groups of an XCD (when the groups split evenly over the 8 XCDs):
+  // the long chains then start first and run alone on their CUs, and the
+  // short blocks fill in behind them.
+  int gq, mi, hkv, b;
+  const int groups = p.B * p.Hkv;
+  if (p.causal && groups % kXcds == 0) {
+    const int xcd = (int)blockIdx.x % kXcds, j = (int)blockIdx.x / kXcds;  // j: dispatch order in the XCD
+    const int ng = groups / kXcds;
+    mi = j / (ng * p.G);
+    const int rest = j % (ng * p.G);
+    const int hg = xcd * ng + rest / p.G;
+    gq = rest % p.G;
+    hkv = hg % p.Hkv;
+    b = hg / p.Hkv;
+  } else {
+    int w = xcd_remap(blockIdx.x, p.total_work);
+    gq = w % p.G;
+    w /= p.G;
+    mi = w % p.num_mblk;
+    w /= p.num_mblk;
+    hkv = w % p.Hkv;
+    b = w / p.Hkv;
+  }
   const int hq = hkv * p.G + gq;
   const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
   const int m0 = mblk * BM;

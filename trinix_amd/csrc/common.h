@@ -73,13 +73,14 @@ struct F16 {
 template <class E>
 __device__ inline float round_to(float x) { return E::lo(E::pack(x, 0.f)); }
 
-// Workgroups are dispatched round-robin over the 8 XCDs (WG x runs on XCD
-// x % 8).  Give each XCD one contiguous range of the work list, so work
-// items that read the same K/V (neighbouring items) share that XCD's L2.
+// Workgroups are dispatched round-robin over the kXcds = 8 XCDs of an
+// MI355X (WG x runs on XCD x % 8).  Give each XCD one contiguous range of the
+// work list, so work items that read the same K/V (neighbouring items) share
+// that XCD's L2.
+constexpr int kXcds = 8;
 __device__ inline int xcd_remap(int x, int total) {
-  constexpr int kXcd = 8;
-  const int xcd = x % kXcd, idx = x / kXcd;
-  const int per = total / kXcd, rem = total % kXcd;
+  const int xcd = x % kXcds, idx = x / kXcds;
+  const int per = total / kXcds, rem = total % kXcds;
   return xcd * per + (xcd < rem ? xcd : rem) + idx;
 }
 
