@@ -250,7 +250,7 @@ int trinix_alibi_bias(const float* slopes, int64_t slope_stride, int64_t nheads,
 
 /* Tile shape the library launches for (head_dim, dtype). */
 typedef struct trinix_tile_cfg {
-  int32_t block_m;      /* query rows per workgroup     */
+  int32_t block_m;      /* query rows per workgroup (large-problem shape) */
   int32_t block_n;      /* keys per K/V tile            */
   int32_t block_d;      /* head_dim the kernel runs at  */
   int32_t waves;        /* wavefronts per workgroup     */

@@ -430,3 +430,57 @@ def test_dropout_matches_philox_oracle(dtype):
     assert (out.cpu().double() - ref).abs().max().item() <= tol
     frac = keep.mean().item()
     assert abs(frac - (1 - p)) < 0.02
+
+
+KS_CASES = [
+    # (B, Sq, Sk, H, Hkv, D, causal, window, features)
+    (2, 1024, 1024, 3, 3, 64, True, None, ""),
+    (1, 700, 700, 4, 2, 64, True, (200, 0), "alibi"),
+    (2, 333, 333, 2, 1, 64, False, None, "mask"),
+    (1, 257, 400, 2, 2, 64, False, (50, 70), "alibi,mask"),
+    (1, 190, 190, 2, 2, 64, True, None, "lse"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", KS_CASES, ids=[str(c) for c in KS_CASES])
+def test_key_split_configs(case, dtype, monkeypatch):
+    """Head_dim 64 small grids split each 32-row group's keys between two
+    wavefronts (ks = 2) and merge the halves through LDS; both tile configs
+    are forced through TRINIX_ATTN_CFG and checked against the oracle, and
+    against each other."""
+    B, Sq, Sk, H, Hkv, D, causal, window, feats = case
+    q, k, v = rand((B, Sq, H, D), dtype, 101), rand((B, Sk, Hkv, D), dtype, 102), rand((B, Sk, Hkv, D), dtype, 103)
+    kw = dict(causal=causal, window_size=window)
+    if "alibi" in feats:
+        kw["alibi_slopes"] = orc.alibi_slopes(H)
+    if "mask" in feats:
+        g = torch.Generator().manual_seed(104)
+        m = torch.randn((Sq, Sk), generator=g)
+        m[torch.rand((Sq, Sk), generator=g) < 0.2] = float("-inf")
+        nb = -(-Sk // 64)
+        blk = (torch.rand((-(-Sq // 64), nb), generator=g) < 0.3).repeat_interleave(64, 0).repeat_interleave(64, 1)
+        m[blk[:Sq, :Sk]] = float("-inf")
+        m[:, 0] = 0
+        if window is not None:  # every row keeps its diagonal key, inside any window
+            m[torch.arange(Sq), torch.arange(Sq).clamp(max=Sk - 1)] = 0
+        kw["attn_mask"] = m
+    outs = {}
+    for ks in (1, 2):
+        monkeypatch.setenv("TRINIX_ATTN_CFG", f"4,2,64,{ks}")
+        dkw = {a: (b.to(DEV) if torch.is_tensor(b) else b) for a, b in kw.items()}
+        out, lse = triton_attn_func(q, k, v, return_lse=True, **dkw)
+        outs[ks] = (out, lse)
+    monkeypatch.delenv("TRINIX_ATTN_CFG")
+    ref = oracle_on(q, k, v, **kw)
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), **kw)
+    for ks in (1, 2):
+        assert_parity_or_more_accurate(outs[ks][0], ref, x64, dtype, f"{case} ks={ks}")
+    d = (outs[1][0].float() - outs[2][0].float()).abs()
+    ok = ~torch.isnan(outs[1][0].float())
+    assert torch.equal(torch.isnan(outs[1][0]), torch.isnan(outs[2][0]))
+    assert d[ok].max().item() <= 2e-2
+    l1, l2 = outs[1][1], outs[2][1]
+    fin = torch.isfinite(l1)
+    assert torch.equal(fin, torch.isfinite(l2))
+    assert (l1[fin] - l2[fin]).abs().max().item() <= 1e-2

@@ -275,17 +275,22 @@ int check_tensor(const void* ptr, const int64_t st[4], int esize) {
 }
 
 // Tile configuration of the 16-bit kernel: 4 wavefronts x 32 query rows,
-// 64-key tiles, 2 wavefronts per SIMD (1 for head_dim 256).
-// TRINIX_ATTN_CFG="nw,occ,bn" overrides the choice (tuning only; a
+// 64-key tiles, 2 wavefronts per SIMD (1 for head_dim 256).  A small grid at
+// head_dim 64 -- no more 128-row workgroups than CUs -- splits each 32-row
+// group's keys between two wavefronts (ks = 2, 64 rows per workgroup): twice
+// the workgroups, half the longest chain of tiles, at twice the K/V copies
+// per flop.  Measured at head_dim 64, bf16: 128 workgroups at S = 4096..16384
+// +50..62%, 64 workgroups at S = 1024 +2%, 384 workgroups (S = 1024) -3%.
+// TRINIX_ATTN_CFG="nw,occ,bn[,ks]" overrides the choice (tuning only; a
 // configuration that is not built is rejected with TRINIX_ERR_BAD_ARGUMENT).
+constexpr int64_t kSmallGrid = 256;  // CUs of an MI355X
 Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq) {
-  Cfg16 c{4, head_dim == 256 ? 1 : 2, 64};
-  (void)batch;
-  (void)hq;
-  (void)sq;
+  Cfg16 c{4, head_dim == 256 ? 1 : 2, 64, 1};
+  if (head_dim == 64 && batch * hq * ((sq + 127) / 128) <= kSmallGrid) c.ks = 2;
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
-    int nw = 0, occ = 0, bn = 0;
-    if (sscanf(env, "%d,%d,%d", &nw, &occ, &bn) == 3) c = Cfg16{nw, occ, bn};
+    int nw = 0, occ = 0, bn = 0, ks = 1;
+    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &ks) >= 3 && nw > 0 && ks > 0 && nw % ks == 0)
+      c = Cfg16{nw, occ, bn, ks};
   }
   return c;
 }
@@ -363,11 +368,11 @@ int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* ou
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
   if (dtype == TRINIX_BF16 || dtype == TRINIX_F16) {
     const Cfg16 c = pick_cfg16(head_dim, 1 << 20, 1, 1 << 20);  // large-problem choice
-    out->block_m = 32 * c.nw;
+    out->block_m = 32 * c.nw / c.ks;
     out->block_n = c.bn;
     out->block_d = (int32_t)head_dim;
     out->waves = c.nw;
-    out->lds_bytes = (int32_t)(2 * 2 * c.bn * head_dim * 2);
+    out->lds_bytes = (int32_t)(2 * 2 * c.ks * c.bn * head_dim * 2);
   } else if (dtype == TRINIX_F32) {
     out->block_m = 32 * kWavesF32;
     out->block_n = 32;
@@ -402,7 +407,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.G = p.Hq / p.Hkv;
   const bool f32 = a->dtype == TRINIX_F32;
   const Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q);
-  const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw;
+  const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw / cfg.ks;
   p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
   const int64_t total = (int64_t)p.B * p.Hq * p.num_mblk;
   if (total >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;

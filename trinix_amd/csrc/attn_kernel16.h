@@ -42,9 +42,14 @@
 
 namespace trinix {
 
-template <class E, int D, int BN, int NW, int OCC, bool ALIBI, bool MASK, bool DROP>
+template <class E, int D, int BN, int NW, int OCC, int KS, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
-  constexpr int BM = NW * 32;  // query rows per workgroup
+  // KS = 2 splits each 32-row group's keys between two wavefronts: wavefront
+  // 2r + kp owns rows 32r..32r+31 and the tiles t_lo + KS*s + kp; the halves
+  // merge through LDS at the end.  It halves the longest dependency chain of
+  // small problems (few row blocks, long causal rows).
+  static_assert(KS == 1 || KS == 2, "key split");
+  constexpr int BM = NW * 32 / KS;  // query rows per workgroup
   constexpr int DS = D / 16;   // MFMA k-steps over head_dim (QK^T)
   constexpr int NB = BN / 32;  // 32-key blocks per tile
   constexpr int DB = D / 32;   // 32-wide head_dim blocks of O^T
@@ -57,10 +62,11 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // Four separate LDS objects (not one array indexed by parity) so that the
   // compiler can tell the buffer being read from the one an asynchronous
   // global->LDS load is filling, and does not wait for that load.
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_k0[BN * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[BN * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[BN * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[BN * D];
+  // With KS = 2 each buffer holds the step's two tiles (tile kp at kp*BN*D).
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k0[KS * BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[KS * BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[KS * BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[KS * BN * D];
   // Tile t lives in buffer slot (t - t_lo) & 1 of K and of V.  `slot` is a
   // std::integral_constant in the full-tile loop (static buffer choice) and
   // an int in the edge loops.
@@ -76,6 +82,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane & 31, g = lane >> 5;
+  const int kp = wave % KS;  // key parity of this wavefront (KS = 2)
 
   // work item: (b, kv-head, m-block, q-head within the group).  Each XCD owns
   // whole KV-head groups, so the q-heads sharing a KV head run on one XCD and
@@ -106,7 +113,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   const int hq = hkv * p.G + gq;
   const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
   const int m0 = mblk * BM;
-  const int iw0 = m0 + wave * 32;
+  const int iw0 = m0 + (wave / KS) * 32;
   const int iwl = min(iw0 + 31, p.Sq - 1);
   const int i = iw0 + r;
   const int ic = min(i, p.Sq - 1);
@@ -507,24 +514,30 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
 
   // ---- main loop -----------------------------------------------------------
-  // Tile t sits in buffer slot (t - t_lo) & 1 of K and V.  Step t: wait for
-  // K[t], V[t]; barrier (every wavefront done with tile t-1, whose buffers
-  // now take the loads of K[t+1], V[t+1]); S = K[t] Q^T; softmax; O += V[t]^T P.
-  auto step = [&](auto pred_c, auto slot, int t) __attribute__((always_inline)) {
+  // Step s covers tiles T = t_lo + KS*s .. T + KS - 1 (this wavefront's tile
+  // is T + kp), held in buffer slot s & 1 of K and V.  Step s: wait for the
+  // step's tiles; barrier (every wavefront done with step s-1, whose buffers
+  // now take the loads of step s+1); S = K Q^T; softmax; O += V^T P.
+  auto step = [&](auto pred_c, auto slot, int T) __attribute__((always_inline)) {
     auto other = [&]() {
       if constexpr (std::is_integral_v<decltype(slot)>) return 1 - slot;
       else return std::integral_constant<int, 1 - decltype(slot)::value>{};
     }();
+    const int t = T + kp;
     if constexpr (MASK && D <= 128)
       if (bm_row && (t + 1) * NCB - bm_c0 > 64) bm_fetch(t * NCB);  // next 64 columns, before the wait
-    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of K[t], V[t] landed
-    __syncthreads();                // ... and every wavefront's; buffers of t-1 are free
-    if (t + 1 < t_hi) {
-      load_k(kbuf(other), t + 1);
-      load_v(vbuf(other), t + 1);
-    }
-    if (tile_live(t)) {
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of the step's tiles landed
+    __syncthreads();                // ... and every wavefront's; buffers of step s-1 are free
+#pragma unroll
+    for (int u = 0; u < KS; ++u)
+      if (T + KS + u < t_hi) {
+        load_k(kbuf(other) + u * BN * D, T + KS + u);
+        load_v(vbuf(other) + u * BN * D, T + KS + u);
+      }
+    if (t < t_hi && tile_live(t)) {
       const int n0 = t * BN;
+      uint16_t* kt = kbuf(slot) + kp * BN * D;
+      uint16_t* vt = vbuf(slot) + kp * BN * D;
       // MFMA sections at raised priority: the other wavefront on this SIMD
       // fills the MFMA pipe gaps with its softmax VALU work.
       const int mcode = MASK ? mask_code(t) : 0;
@@ -532,8 +545,8 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
         f32x16_t sc[NB];
         u32x4_t vpre[VPF];
         __builtin_amdgcn_s_setprio(1);
-        qk(kbuf(slot), n0, sc);
-        vprefetch(vbuf(slot), vpre);  // V operand reads in flight during the softmax
+        qk(kt, n0, sc);
+        vprefetch(vt, vpre);  // V operand reads in flight during the softmax
         __builtin_amdgcn_s_setprio(0);
         u32x4_t pb[NB][2];
         // At D = 64 (registers to spare) a full tile whose mask blocks are
@@ -546,35 +559,73 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
           softmax(pred_c, std::bool_constant<MASK>{}, sc, n0, mcode, pb);
         }
         __builtin_amdgcn_s_setprio(1);
-        pv(vbuf(slot), pb, vpre);
+        pv(vt, pb, vpre);
         __builtin_amdgcn_s_setprio(0);
       }
     }
   };
   if constexpr (MASK && D <= 128)
-    if (bm_row) bm_fetch(t_lo * NCB);
-  if (t_lo < t_hi) {
-    load_k(kbuf(std::integral_constant<int, 0>{}), t_lo);
-    load_v(vbuf(std::integral_constant<int, 0>{}), t_lo);
+    if (bm_row) bm_fetch((t_lo + kp) * NCB);
+#pragma unroll
+  for (int u = 0; u < KS; ++u)
+    if (t_lo + u < t_hi) {
+      load_k(kbuf(std::integral_constant<int, 0>{}) + u * BN * D, t_lo + u);
+      load_v(vbuf(std::integral_constant<int, 0>{}) + u * BN * D, t_lo + u);
+    }
+  // Steps whose tiles are all full run the straight-line body, in pairs
+  // starting at an even step so that their buffer slots are static (the full
+  // range is trimmed to start at an even step and to an even length; trimmed
+  // steps run the edge body, which is always exact).
+  const int s_hi = (t_hi - t_lo + KS - 1) / KS;
+  int s_flo = (t_flo - t_lo + KS - 1) / KS;
+  int s_fhi = max(s_flo, (t_fhi - t_lo) / KS);
+  if ((s_flo & 1) && s_flo < s_fhi) ++s_flo;
+  s_fhi -= (s_fhi - s_flo) & 1;
+  int si = 0;
+  for (; si < s_flo; ++si) step(std::true_type{}, si & 1, t_lo + KS * si);
+  for (; si < s_fhi; si += 2) {
+    step(std::false_type{}, std::integral_constant<int, 0>{}, t_lo + KS * si);
+    step(std::false_type{}, std::integral_constant<int, 1>{}, t_lo + KS * (si + 1));
   }
-  // Full tiles run in pairs starting at an even offset from t_lo, so their
-  // buffer slots are static (the full range is trimmed to start at an even
-  // offset and to an even length; trimmed tiles run as edge tiles, which are
-  // always exact).
-  if (((t_flo - t_lo) & 1) && t_flo < t_fhi) ++t_flo;
-  t_fhi -= (t_fhi - t_flo) & 1;
-  int t = t_lo;
-  for (; t < t_flo; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
-  for (; t < t_fhi; t += 2) {
-    step(std::false_type{}, std::integral_constant<int, 0>{}, t);
-    step(std::false_type{}, std::integral_constant<int, 1>{}, t + 1);
+  for (; si < s_hi; ++si) step(std::true_type{}, si & 1, t_lo + KS * si);
+
+  if constexpr (KS == 2) {
+    // Merge the two key halves of each row group: wavefront 2r+1 hands its
+    // (m, l, O) to wavefront 2r through LDS (the K buffers are free once every
+    // wavefront has passed the barrier).  Lane-for-lane: both hold the same
+    // rows and head_dim columns.
+    float* mo = (float*)lds_k0;  // [row group][DB*16][64 lanes]
+    float* ml = (float*)lds_v0;  // [row group][2][64 lanes]
+    const int rg = wave / KS;
+    __syncthreads();
+    if (kp == 1) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mo[((rg * DB + db) * 16 + v) * 64 + lane] = acc[db][v];
+      ml[(rg * 2 + 0) * 64 + lane] = m_run;
+      ml[(rg * 2 + 1) * 64 + lane] = l_run;
+    }
+    __syncthreads();
+    if (kp == 0) {
+      const float m1 = ml[(rg * 2 + 0) * 64 + lane], l1 = ml[(rg * 2 + 1) * 64 + lane];
+      const float m = fmaxf(m_run, m1);
+      // a half that saw no allowed key has m = -inf and contributes 0
+      const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m);
+      const float a1 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - m);
+      l_run = l_run * a0 + l1 * a1;
+      m_run = m;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[db][v] = acc[db][v] * a0 + mo[((rg * DB + db) * 16 + v) * 64 + lane] * a1;
+    }
   }
-  for (; t < t_hi; ++t) step(std::true_type{}, (t - t_lo) & 1, t);
 
   // Epilogue: O = acc / l (NaN for rows with no allowed key, like the eager
   // softmax over an all -inf row), optional log-sum-exp.
   const float l = xlane_sum(l_run);
-  if (i < p.Sq) {
+  if (i < p.Sq && kp == 0) {
     const float inv = 1.f / l;
     uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)i * p.o_ss;
 #pragma unroll
@@ -590,14 +641,14 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   }
 }
 
-// Launcher of the (nw, occ) = (4, 2) tile shape: every feature combination.
-template <class E, int D, int BN, int NW, int OCC>
+// Launcher of one tile shape: every feature combination.
+template <class E, int D, int BN, int NW, int OCC, int KS>
 hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   const dim3 grid((unsigned)p.total_work), block(NW * 64);
   switch (feat) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,         \
+    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,     \
                                         (F & kFeatDropout) != 0>),                                              \
                        grid, block, 0, st, p);                                                                  \
     return hipGetLastError();
@@ -614,15 +665,20 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   }
 }
 
-// Tile config built per (dtype, D), every feature combination:
-// (nw, occ, bn) = (4, 2, 64) for D <= 128; (4, 1, 64) for D = 256, whose Q
-// fragment (64 VGPRs) and O accumulator (128) need one wavefront per SIMD,
-// and whose double-buffered K/V tiles take 128 KiB of LDS.
-#define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                              \
-  hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                           \
-    constexpr int kOcc = (D) == 256 ? 1 : 2;                                                          \
-    if (cfg.bn == 64 && cfg.nw == 4 && cfg.occ == kOcc) return launch_feat<E, D, 64, 4, kOcc>(p, feat, st); \
-    return hipErrorInvalidValue;                                                                        \
+// Tile configs built per (dtype, D), every feature combination:
+// (nw, occ, bn, ks) = (4, 2, 64, 1) for D <= 128; (4, 1, 64, 1) for D = 256,
+// whose Q fragment (64 VGPRs) and O accumulator (128) need one wavefront per
+// SIMD, and whose double-buffered K/V tiles take 128 KiB of LDS; and for D = 64
+// also (4, 2, 64, 2), the key split for small grids (64 KiB of LDS: two
+// tiles per buffer).
+#define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                                   \
+  hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                                \
+    constexpr int kOcc = (D) == 256 ? 1 : 2;                                                               \
+    if (cfg.bn != 64 || cfg.nw != 4 || cfg.occ != kOcc) return hipErrorInvalidValue;                       \
+    if (cfg.ks == 1) return launch_feat<E, D, 64, 4, kOcc, 1>(p, feat, st);                                \
+    if constexpr ((D) == 64)                                                                               \
+      if (cfg.ks == 2) return launch_feat<E, D, 64, 4, kOcc, 2>(p, feat, st);                              \
+    return hipErrorInvalidValue;                                                                             \
   }
 
 }  // namespace trinix

@@ -40,9 +40,10 @@ struct FwdParams {
 
 // Tile shape of one 16-bit kernel instantiation.
 struct Cfg16 {
-  int nw;   // wavefronts per workgroup (32 query rows each)
+  int nw;   // wavefronts per workgroup (32 query rows per key split)
   int occ;  // target wavefronts per SIMD (register budget 512 / occ)
   int bn;   // keys per K/V tile
+  int ks;   // key split: wavefronts sharing one 32-row group (rows per workgroup = 32 * nw / ks)
 };
 
 __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx) {
