@@ -254,11 +254,32 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
   // paid 128 register moves at the join.
   auto subtile = [&](bool edge, const uint16_t* qt_lds, const uint16_t* ot_lds, const float* l_lds,
                      const float* d_lds, int st, int i0, int hq, float slope_l2, int mcode) __attribute__((always_inline)) {
+    // S = Q K^T, then dP = dO V^T: 2*DS MFMAs whose A operands (Q / dO row
+    // fragments) are read from LDS RPF MFMAs ahead; the sched_group_barriers
+    // keep the reads ahead of their MFMAs (one wavefront per SIMD: nothing
+    // else hides the LDS latency).
+    constexpr int NSD = 2 * DS, RPF = 6;
     f32x16_t s = {}, dp = {};
+    {
+      auto aread = [&](int k) __attribute__((always_inline)) {
+        return k < DS ? rowread(qt_lds, st * 32 + r, k) : rowread(ot_lds, st * 32 + r, k - DS);
+      };
+      u32x4_t af[NSD];
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) s = E::mfma(rowread(qt_lds, st * 32 + r, ds), kr[ds], s);
+      for (int k = 0; k < RPF; ++k) af[k] = aread(k);
 #pragma unroll
-    for (int ds = 0; ds < DS; ++ds) dp = E::mfma(rowread(ot_lds, st * 32 + r, ds), vr[ds], dp);
+      for (int k = 0; k < NSD; ++k) {
+        if (k + RPF < NSD) af[k + RPF] = aread(k + RPF);
+        if (k < DS) s = E::mfma(af[k], kr[k], s);
+        else dp = E::mfma(af[k], vr[k - DS], dp);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, RPF, 0);
+#pragma unroll
+      for (int k = 0; k < NSD; ++k) {
+        if (k + RPF < NSD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    }
     // element v of the lane: query row st*32 + (v/4)*8 + 4g + v%4 of the tile
     const char* mrow = nullptr;
     if constexpr (MASK) {
@@ -305,13 +326,31 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
       zb[kk] = (u32x4_t){E::pack(dz[kk * 8 + 0], dz[kk * 8 + 1]), E::pack(dz[kk * 8 + 2], dz[kk * 8 + 3]),
                          E::pack(dz[kk * 8 + 4], dz[kk * 8 + 5]), E::pack(dz[kk * 8 + 6], dz[kk * 8 + 7])};
     }
+    // dV^T += dO^T P and dK^T += Q^T dZ: 4*DB MFMAs, A operands from LDS
+    // transpose reads issued TPF MFMAs ahead.
+    {
+      constexpr int NTR = 4 * DB, TPF = 4;
+      auto tread = [&](int m) __attribute__((always_inline)) {
+        const int db = m / 4, kk = (m / 2) % 2;
+        return (m & 1) ? trread(qt_lds, st, db, kk) : trread(ot_lds, st, db, kk);
+      };
+      u32x4_t tf[NTR];
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+      for (int m = 0; m < TPF; ++m) tf[m] = tread(m);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        dv[db] = E::mfma(trread(ot_lds, st, db, kk), pb[kk], dv[db]);
-        dk[db] = E::mfma(trread(qt_lds, st, db, kk), zb[kk], dk[db]);
+      for (int m = 0; m < NTR; ++m) {
+        if (m + TPF < NTR) tf[m + TPF] = tread(m + TPF);
+        const int db = m / 4, kk = (m / 2) % 2;
+        if (m & 1) dk[db] = E::mfma(tf[m], zb[kk], dk[db]);
+        else dv[db] = E::mfma(tf[m], pb[kk], dv[db]);
       }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * TPF, 0);
+#pragma unroll
+      for (int m = 0; m < NTR; ++m) {
+        if (m + TPF < NTR) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      }
+    }
   };
 
   // ---- walk the q-heads of the group and the query tiles of the band
