@@ -138,12 +138,13 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   int t_fhi = fhi > 0 ? (int)(fhi / BN) : 0;
   t_flo = min(max(t_flo, t_lo), t_hi);
   t_fhi = min(max(t_fhi, t_flo), t_hi);
-  // Scores in log2 units: x = q.k * c (+ bias).  ALiBi with scale 0 drops the
-  // q.k term (q operand zeroed) and uses c = 1, so that its bias can ride in
-  // the score accumulator (seed_scores) as for any other scale.
-  const bool alibi_zero_scale = ALIBI && p.scale_log2 == 0.f;
-  const float c = alibi_zero_scale ? 1.f : p.scale_log2;
-  if (!(c > 0.f)) t_flo = t_fhi = t_hi;  // raw-max trick needs scale > 0
+  // Scores stay in the raw domain, s = q.k (+ bias / c), and the scale
+  // c = scale * log2 e > 0 is applied in the FMA before the exp, so the max of
+  // the raw scores is the max of the scaled ones.  A negative scale negates
+  // the q operand instead (exact: the sign bits); a zero scale zeroes it and
+  // uses c = 1 (the q.k term is dropped, the biases remain).
+  const bool q_neg = p.scale_log2 < 0.f, q_zero = p.scale_log2 == 0.f;
+  const float c = q_neg ? -p.scale_log2 : (q_zero ? 1.f : p.scale_log2);
 
   // Q row in registers: qr[ds] = q[i][ds*16 + g*8 .. +8].
   u32x4_t qr[DS];
@@ -181,7 +182,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
         qr[ds + DS / 2] = x2;
       }
     }
-    if (alibi_zero_scale)
+    if (q_neg)
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) qr[ds] ^= (u32x4_t){0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
+    if (q_zero)
 #pragma unroll
       for (int ds = 0; ds < DS; ++ds) qr[ds] = (u32x4_t){};
   }
@@ -402,45 +406,44 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     for (int m = 0; m < VPF; ++m) vpre[m] = vread(vt, m);
   };
 
-  // Softmax update of one tile; writes P^T packed as the PV B operand.
-  // GENERIC (edge tile, or a tile that reads the mask): x = s*c + mask (or
-  // -inf where not allowed); plain full tiles keep raw scores, take the max
-  // of the raw scores (c > 0) and fold the scale into one FMA before the exp.
-  // ALiBi is in the scores already (seed_scores).
+  // Softmax update of one tile; writes P^T packed as the PV B operand.  All
+  // in the raw-score domain: a tile that reads the mask adds mask * log2e / c
+  // to its raw scores, an edge tile sets the scores it may not see to -inf;
+  // the row max is taken on the raw scores and the scale folds into one FMA
+  // before the exp.  ALiBi is in the scores already (seed_scores).
   auto softmax = [&](auto pred_c, auto mask_c, f32x16_t(&s)[NB], int n0, int mcode, u32x4_t(&pb)[NB][2])
                      __attribute__((always_inline)) {
     constexpr bool PRED = decltype(pred_c)::value;
     constexpr bool MASKC = decltype(mask_c)::value;
-    constexpr bool GENERIC = PRED || MASKC;
-    float mx = -INFINITY;
-    if constexpr (GENERIC) {
+    if constexpr (MASKC) {
+      if (mcode > 0) {
+        const float mscale = kLog2e / c;  // mask in the raw-score domain
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-          const int j0 = n0 + nb * 32 + vq * 8 + g * 4;
-          float mv[4] = {0.f, 0.f, 0.f, 0.f};
-          if constexpr (MASKC) {
-            if (mcode > 0) load_mask4(mrow, p.mask_dtype, j0, p.mk_sj, p.Sk - 1, mv);
+          for (int vq = 0; vq < 4; ++vq) {
+            float mv[4];
+            load_mask4(mrow, p.mask_dtype, n0 + nb * 32 + vq * 8 + g * 4, p.mk_sj, p.Sk - 1, mv);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = __builtin_fmaf(mv[e], mscale, s[nb][vq * 4 + e]);
           }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = j0 + e;
-            float x = s[nb][vq * 4 + e] * c;
-            if constexpr (MASKC) x += mv[e] * kLog2e;
-            if constexpr (PRED) x = (uint32_t)(j - jlo) <= jspan ? x : -INFINITY;
-            s[nb][vq * 4 + e] = x;
-            mx = fmaxf(mx, x);
-          }
-        }
-      mx = xlane_max(mx);
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[nb][v]);
-      mx = xlane_max(mx) * c;  // raw max scaled: c > 0 on this path
+      }
     }
+    if constexpr (PRED) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int j = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          s[nb][v] = (uint32_t)(j - jlo) <= jspan ? s[nb][v] : -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[nb][v]);
+    mx = xlane_max(mx) * c;  // raw max scaled (c > 0)
     // Lazy rescale: keep the running max unless this tile exceeds it by TAU.
     if (__builtin_expect(wave_any(mx > m_run + TAU), 0)) {
       const float m_new = fmaxf(m_run, mx);
@@ -452,14 +455,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
       for (int db = 0; db < DB; ++db) acc[db] *= alpha;
       m_run = m_new;
     }
-    if constexpr (GENERIC) {
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) s[nb][v] = __builtin_amdgcn_exp2f(s[nb][v] - m_use);
-    } else {
-      const float mneg = -m_run;
+    {
+      // a row that has seen no allowed key keeps -inf scores: exp2(-inf) = 0
+      const float mneg = m_run == -INFINITY ? 0.f : -m_run;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -549,15 +547,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
         vprefetch(vt, vpre);  // V operand reads in flight during the softmax
         __builtin_amdgcn_s_setprio(0);
         u32x4_t pb[NB][2];
-        // At D = 64 (registers to spare) a full tile whose mask blocks are
-        // all zero runs the plain softmax; larger head dims keep one softmax
-        // body, as two would spill.
-        if constexpr (MASK && D <= 64 && !decltype(pred_c)::value) {
-          if (mcode == 0) softmax(pred_c, std::false_type{}, sc, n0, mcode, pb);
-          else softmax(pred_c, std::true_type{}, sc, n0, mcode, pb);
-        } else {
-          softmax(pred_c, std::bool_constant<MASK>{}, sc, n0, mcode, pb);
-        }
+        softmax(pred_c, std::bool_constant<MASK>{}, sc, n0, mcode, pb);
         __builtin_amdgcn_s_setprio(1);
         pv(vt, pb, vpre);
         __builtin_amdgcn_s_setprio(0);
