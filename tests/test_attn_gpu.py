@@ -224,21 +224,36 @@ def test_blockmap_longer_than_64_columns(causal):
 @pytest.mark.parametrize("dtype,D", [(torch.float16, 64), (torch.bfloat16, 128)])
 @pytest.mark.parametrize("scale", [None, 0.0, -0.07, 0.5])
 @pytest.mark.parametrize("causal", [False, True])
-def test_alibi_scales(dtype, D, scale, causal):
-    """ALiBi rides in the score accumulator as bias / scale; zero and negative
-    scales, causal and non-causal, output and log-sum-exp against fp64."""
+@pytest.mark.parametrize("bias", ["alibi", "none", "mask"])
+def test_scales_and_biases(dtype, D, scale, causal, bias):
+    """Scores stay in the raw domain with the scale folded into the exp's FMA
+    (c > 0): a negative scale negates the q operand, a zero scale zeroes it;
+    ALiBi rides in the score accumulator as bias / c and the mask is added as
+    mask * log2e / c.  Output and log-sum-exp against fp64."""
     B, S, H = 1, 300, 4
     q, k, v = rand((B, S, H, D), dtype, 91), rand((B, S, H, D), dtype, 92), rand((B, S, H, D), dtype, 93)
+    kw = dict(causal=causal, softmax_scale=scale)
     slopes = orc.alibi_slopes(H)
-    out, lse = triton_attn_func(q, k, v, alibi_slopes=slopes.to(DEV), causal=causal, softmax_scale=scale,
-                                return_lse=True)
-    ref = oracle_on(q, k, v, alibi_slopes=slopes, causal=causal, softmax_scale=scale)
-    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), alibi_slopes=slopes, causal=causal, softmax_scale=scale)
-    assert_parity_or_more_accurate(out, ref, x64, dtype, f"alibi scale={scale} causal={causal}")
+    m = None
+    if bias == "alibi":
+        kw["alibi_slopes"] = slopes
+    if bias == "mask":
+        g = torch.Generator().manual_seed(94)
+        m = torch.randn((S, S), generator=g) * 3
+        m[torch.rand((S, S), generator=g) < 0.2] = float("-inf")
+        m[:, 0] = 0
+        kw["attn_mask"] = m
+    out, lse = triton_attn_func(q, k, v, return_lse=True, **{a: (b.to(DEV) if torch.is_tensor(b) else b) for a, b in kw.items()})
+    ref = oracle_on(q, k, v, **kw)
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), **kw)
+    assert_parity_or_more_accurate(out, ref, x64, dtype, f"{bias} scale={scale} causal={causal}")
     sc = D ** -0.5 if scale is None else scale
     s = torch.einsum("bihd,bjhd->bhij", q.cpu().double(), k.cpu().double()) * sc
-    ij = (torch.arange(S)[:, None] - torch.arange(S)[None, :]).abs().double()
-    s = s - slopes.double()[None, :, None, None] * ij
+    if bias == "alibi":
+        ij = (torch.arange(S)[:, None] - torch.arange(S)[None, :]).abs().double()
+        s = s - slopes.double()[None, :, None, None] * ij
+    if bias == "mask":
+        s = s + m.double()
     if causal:
         s.masked_fill_(torch.triu(torch.ones(S, S), 1).bool(), float("-inf"))
     want = torch.logsumexp(s, dim=-1)
