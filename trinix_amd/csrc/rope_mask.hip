@@ -112,10 +112,17 @@ __global__ __launch_bounds__(256) void rope_scalar_kernel(const T* x, int64_t xs
   S::st(orow, d + half, rope_hi<S>(a, bb, c, sn));
 }
 
-// One workgroup per 32x64 block; 8 elements per thread.
+// One workgroup per 32x64 block; 8 consecutive elements per thread.  `vec`
+// (host-checked: key stride 1, every row start 16-byte aligned) loads them
+// with one or two 16-byte loads (fewer for 8-bit masks); rows that reach
+// past Sk, or strided masks, load element by element.
+__device__ inline void classify(float v, int& all_zero, int& all_ninf) {
+  all_zero &= (v == 0.f);
+  all_ninf &= (v == -INFINITY);
+}
 __global__ __launch_bounds__(256) void blockmap_kernel(const char* mask, int dtype, int64_t sb, int64_t sh,
                                                        int64_t si, int64_t sj, int mh, int Sq, int Sk,
-                                                       int rows, int cols, uint8_t* out) {
+                                                       int rows, int cols, int vec, uint8_t* out) {
   const int cb = blockIdx.x, rb = blockIdx.y, bh = blockIdx.z;
   const int b = bh / mh, h = bh % mh;
   const int tid = threadIdx.x;
@@ -125,19 +132,52 @@ __global__ __launch_bounds__(256) void blockmap_kernel(const char* mask, int dty
   int all_zero = 1, all_ninf = 1;
   if (i < Sq) {
     const char* rowp = mask + (b * sb + h * sh + (int64_t)i * si) * esz;
-    for (int e = 0; e < 8; ++e) {
-      const int j = jb + e;
-      if (j >= Sk) break;
-      float v;
-      const int64_t idx = (int64_t)j * sj;
+    if (vec && jb + 8 <= Sk) {
+      const char* p8 = rowp + (int64_t)jb * esz;
       switch (dtype) {
-        case TRINIX_F32: v = ((const float*)rowp)[idx]; break;
-        case TRINIX_F16: v = (float)((const _Float16*)rowp)[idx]; break;
-        case TRINIX_BF16: v = __uint_as_float(((uint32_t)((const uint16_t*)rowp)[idx]) << 16); break;
-        default: v = (float)((const uint8_t*)rowp)[idx]; break;
+        case TRINIX_F32: {
+          const float4 a = *(const float4*)p8, c = *(const float4*)(p8 + 16);
+          classify(a.x, all_zero, all_ninf); classify(a.y, all_zero, all_ninf);
+          classify(a.z, all_zero, all_ninf); classify(a.w, all_zero, all_ninf);
+          classify(c.x, all_zero, all_ninf); classify(c.y, all_zero, all_ninf);
+          classify(c.z, all_zero, all_ninf); classify(c.w, all_zero, all_ninf);
+          break;
+        }
+        case TRINIX_F16:
+        case TRINIX_BF16: {
+          const uint4 w = *(const uint4*)p8;
+          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = dtype == TRINIX_F16 ? F16::lo(ws[e]) : BF16::lo(ws[e]);
+            const float hi = dtype == TRINIX_F16 ? F16::hi(ws[e]) : BF16::hi(ws[e]);
+            classify(lo, all_zero, all_ninf);
+            classify(hi, all_zero, all_ninf);
+          }
+          break;
+        }
+        default: {
+          const uint2 w = *(const uint2*)p8;
+          // bytes: all zero <=> both words zero; an 8-bit mask is never -inf
+          all_zero &= (w.x == 0u && w.y == 0u);
+          all_ninf = 0;
+          break;
+        }
       }
-      all_zero &= (v == 0.f);
-      all_ninf &= (v == -INFINITY);
+    } else {
+      for (int e = 0; e < 8; ++e) {
+        const int j = jb + e;
+        if (j >= Sk) break;
+        float v;
+        const int64_t idx = (int64_t)j * sj;
+        switch (dtype) {
+          case TRINIX_F32: v = ((const float*)rowp)[idx]; break;
+          case TRINIX_F16: v = (float)((const _Float16*)rowp)[idx]; break;
+          case TRINIX_BF16: v = __uint_as_float(((uint32_t)((const uint16_t*)rowp)[idx]) << 16); break;
+          default: v = (float)((const uint8_t*)rowp)[idx]; break;
+        }
+        classify(v, all_zero, all_ninf);
+      }
     }
   }
   all_zero = __syncthreads_and(all_zero);
@@ -214,11 +254,19 @@ int trinix_attn_mask_blockmap(const void* mask, int32_t mask_dtype, int64_t mb, 
   const int rows = (int)((seqlen_q + TRINIX_BLOCKMAP_ROWS - 1) / TRINIX_BLOCKMAP_ROWS);
   const int cols = (int)((seqlen_k + TRINIX_BLOCKMAP_COLS - 1) / TRINIX_BLOCKMAP_COLS);
   if (rows >= 65536) return TRINIX_ERR_BAD_SHAPE;
+  // 16-byte loads of 8 elements when every row start is 16-byte aligned and
+  // the key stride is 1 (element strides of the batch / head / row axes are
+  // multiples of 16 bytes, or those axes have one entry)
+  const int64_t esz = mask_dtype == TRINIX_F32 ? 4 : (mask_dtype == TRINIX_U8 ? 1 : 2);
+  const int64_t align = mask_dtype == TRINIX_U8 ? 8 : 16;
+  auto aligned = [&](int64_t s, int64_t n) { return n <= 1 || (s * esz) % align == 0; };
+  const int vec = stride[3] == 1 && ((uintptr_t)mask % align) == 0 && aligned(stride[0], mb) &&
+                  aligned(stride[1], mh) && aligned(stride[2], seqlen_q);
   hipStream_t st = (hipStream_t)stream;
   (void)hipGetLastError();
   hipLaunchKernelGGL(blockmap_kernel, dim3(cols, rows, (unsigned)(mb * mh)), dim3(256), 0, st, (const char*)mask,
                      (int)mask_dtype, stride[0], stride[1], stride[2], stride[3], (int)mh, (int)seqlen_q,
-                     (int)seqlen_k, rows, cols, out);
+                     (int)seqlen_k, rows, cols, vec, out);
   return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }
 
