@@ -151,6 +151,9 @@ def fwd_bwd_ms(w, inp, torch, iters=10):
         kw.update(rotary_cos=inp.cos, rotary_sin=inp.sin)
 
     def step():
+        # gradients start from None each step, as after optimizer.zero_grad()
+        # (set_to_none=True, its default): no accumulation kernels are timed
+        q.grad = k.grad = v.grad = None
         triton_attn_func(q, k, v, **kw).backward(do)
 
     for _ in range(3):

@@ -9,14 +9,17 @@
 //   dK = scale * dZ^T Q,  dQ = scale * dZ K.
 // Three launches, no atomics (deterministic):
 //   bwd_delta  delta[b, h, i] = sum_d dO*O (fp32);
-//   bwd_dkdv   one workgroup per (batch, kv-head, 128 keys): each wavefront
-//              keeps its 32 keys' K and V rows in registers and walks every
-//              q-head of its group and every query tile of the band, so dK
-//              and dV of a KV head are summed in registers (GQA included);
+//   bwd_dkdv   one workgroup of 8 wavefronts per (batch, kv-head, 128
+//              keys): per 32 keys one wavefront computes P and dV (K rows in
+//              registers), a second one dP, dZ and dK (V rows in registers)
+//              from the first one's P; both walk every q-head of the group
+//              and every query tile of the band, so dK and dV of a KV head
+//              are summed in registers (GQA included);
 //   bwd_dq     one workgroup per (batch, q-head, 128 query rows), the
 //              forward's shape: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
 // All products run on v_mfma_f32_32x32x16_{bf16,f16}; P and dZ are rounded to
-// the input dtype for their products, as in the forward.
+// the input dtype for their products, as in the forward.  bwd_dkdv also takes
+// dZ = P (dP - delta) from the rounded P (bwd_dq from the fp32 one).
 #pragma once
 #include <climits>
 
@@ -128,32 +131,44 @@ struct TileReader {
 };
 
 // ---------------------------------------------------------------------------
-// dK, dV.  Lane l of wavefront w owns key j = kb0 + 32w + l%32.  Per 32-query
-// sub-tile: S = Q K^T and dP = dO V^T with the query rows on the MFMA rows
-// (A operand: Q / dO rows read from LDS) and keys on the columns (B operand:
-// the lane's K / V row in registers), so S, dP, P and dZ of a lane are its
-// key's column; dV^T += dO^T P and dK^T += Q^T dZ take P / dZ straight from
-// those registers as the B operand and dO^T / Q^T through LDS transpose reads.
+// dK, dV: a two-stage pipeline over two wavefronts per 32-key group.  Lane l
+// of either wavefront of group kg owns key j = kb0 + 32kg + l%32.  Per
+// 32-query sub-tile, with the query rows on the MFMA rows (A operand: Q / dO
+// rows read from LDS) and the keys on the columns (B operand: the lane's K /
+// V row in registers):
+//   stage A (waves 0..NG-1):   S = Q K^T, P = exp(scale*S + bias - lse),
+//                              dV^T += dO^T P, and P (in the input dtype) to
+//                              LDS;
+//   stage B (waves NG..2NG-1): dP = dO V^T, dZ = P (dP - delta) with stage A's
+//                              P, dK^T += Q^T dZ;
+// stage B runs one item (one query tile of one q-head) behind stage A.  Wave
+// w and w + NG share a SIMD (the 8 wavefronts of the workgroup go round-robin
+// over its 4 SIMDs), so every SIMD holds one wavefront of each stage, 16
+// MFMAs per sub-tile each, and one's softmax VALU work overlaps the other's
+// MFMAs.  dO^T and Q^T come from LDS transpose reads.
+// Q/dO/lse/delta tiles rotate through NSL = 3 LDS slots (stage A's item,
+// stage B's item, the item being loaded) and P through 2; one barrier per
+// item orders all of it.  The loop runs six steps per trip so that every slot
+// index is a compile-time constant (LDS addresses as immediate offsets).
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK>
-__global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
-  constexpr int NW = 4, BK = NW * 32, BQ = 64;
-  constexpr int DS = D / 16, DB = D / 32, UPR = D / 8;
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
+  constexpr int NW = 8, NG = NW / 2, BK = NG * 32, BQ = 64, NSL = 3, NST = BQ / 32;
+  constexpr int DS = D / 16, DB = D / 32, UPR = D / 8, TILE = BQ * D;
   constexpr int LPW = BQ * UPR / (64 * NW);  // 16-byte copies per wavefront per Q (or dO) tile
+  constexpr int RPF = 4, TPF = 2;            // row / transpose operand reads issued ahead of their MFMA
   static_assert(LPW >= 1 && BQ * UPR % (64 * NW) == 0, "tile shape");
 
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_q0[BQ * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_q1[BQ * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_o0[BQ * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_o1[BQ * D];
-  __shared__ __attribute__((aligned(256))) float lds_l0[BQ];
-  __shared__ __attribute__((aligned(256))) float lds_l1[BQ];
-  __shared__ __attribute__((aligned(256))) float lds_d0[BQ];
-  __shared__ __attribute__((aligned(256))) float lds_d1[BQ];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_q[NSL * TILE];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_o[NSL * TILE];
+  __shared__ __attribute__((aligned(1024))) u32x4_t lds_p[2 * NG * NST * 2 * 64];
+  __shared__ __attribute__((aligned(256))) float lds_l[NSL * BQ];
+  __shared__ __attribute__((aligned(256))) float lds_d[NSL * BQ];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & 31, g = lane >> 5;
+  const int kg = wave % NG;
+  const int g = lane >> 5;
 
   int w = xcd_remap(blockIdx.x, p.B * p.Hkv * p.num_kblk);
   const int kblk = w % p.num_kblk;  // causal: low key blocks see the most queries, and run first
@@ -161,8 +176,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
   const int hkv = w % p.Hkv;
   const int b = w / p.Hkv;
   const int kb0 = kblk * BK;
-  const int j0 = kb0 + wave * 32;
-  const int j = j0 + r;
+  const int j0 = kb0 + kg * 32;
+  const int j = j0 + (lane & 31);
   const int jc = min(j, p.Sk - 1);
   const Band band(p);
   // queries this lane's key may see: j - dhi <= i <= j - dlo, 0 <= i < Sq (none if j >= Sk)
@@ -170,28 +185,14 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
                               : Span(1, 0);
   const float c = p.scale_log2;
 
-  // this lane's K and V rows (B operands of S and dP)
-  u32x4_t kr[DS], vr[DS];
-  {
-    const uint16_t* krow = p.k + b * p.k_sb + hkv * p.k_sh + (int64_t)jc * p.k_ss;
-    const uint16_t* vrow = p.v + b * p.v_sb + hkv * p.v_sh + (int64_t)jc * p.v_ss;
-#pragma unroll
-    for (int ds = 0; ds < DS; ++ds) {
-      kr[ds] = *(const u32x4_t*)(krow + ds * 16 + g * 8);
-      vr[ds] = *(const u32x4_t*)(vrow + ds * 16 + g * 8);
-    }
-  }
-  f32x16_t dk[DB], dv[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) dk[db] = dv[db] = (f32x16_t){};
-
   // Query range of the workgroup's keys [kb0, kb0 + BK): i - j in [-dhi, -dlo].
   const int kmax = min(kb0 + BK, p.Sk) - 1;
-  int i_lo = (int)max((int64_t)0, (int64_t)kb0 - band.dhi);
-  int i_hi = (int)min((int64_t)p.Sq, (int64_t)kmax - band.dlo + 1);
+  const int i_lo = (int)max((int64_t)0, (int64_t)kb0 - band.dhi);
+  const int i_hi = (int)min((int64_t)p.Sq, (int64_t)kmax - band.dlo + 1);
   const int qt_lo = i_lo / BQ;
   const int qt_hi = i_hi > i_lo ? (i_hi + BQ - 1) / BQ : qt_lo;
   const int nqt = qt_hi - qt_lo;
+  const int n_items = nqt > 0 ? p.G * nqt : 0;  // item = (q-head of the group, query tile)
 
   // ---- tile copies: Q and dO rows (16-byte units, swizzled), lse and delta
   auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
@@ -213,206 +214,251 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkdv(const BwdParams p) {
     const uint32_t row = (uint32_t)min(lane, p.Sq - 1 - i0);
     dma_4b_s(row * 4u, gb, __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)lds_vec));
   };
-  auto load_tile = [&](auto slot_c, int hq, int qt) __attribute__((always_inline)) {
+  struct Item {
+    int gh, qt;
+  };
+  auto next_item = [&](Item it) __attribute__((always_inline)) {
+    return it.qt + 1 < qt_hi ? Item{it.gh, it.qt + 1} : Item{it.gh + 1, qt_lo};
+  };
+  auto load_item = [&](Item it, auto slot_c) __attribute__((always_inline)) {
     constexpr int SL = decltype(slot_c)::value;
-    const int i0 = qt * BQ;
-    load_rows(p.q + b * p.q_sb + hq * p.q_sh, p.q_ss, SL ? lds_q1 : lds_q0, i0);
-    load_rows(p.dout + b * p.do_sb + hq * p.do_sh, p.do_ss, SL ? lds_o1 : lds_o0, i0);
+    const int hq = hkv * p.G + it.gh, i0 = it.qt * BQ;
+    load_rows(p.q + b * p.q_sb + hq * p.q_sh, p.q_ss, lds_q + SL * TILE, i0);
+    load_rows(p.dout + b * p.do_sb + hq * p.do_sh, p.do_ss, lds_o + SL * TILE, i0);
     const int64_t vo = ((int64_t)b * p.Hq + hq) * p.Sq;
-    if (wave == 0) load_vec(p.lse + vo, SL ? lds_l1 : lds_l0, i0);
-    if (wave == 1) load_vec(p.delta + vo, SL ? lds_d1 : lds_d0, i0);
+    if (wave == 0) load_vec(p.lse + vo, lds_l + SL * BQ, i0);
+    if (wave == 1) load_vec(p.delta + vo, lds_d + SL * BQ, i0);
+  };
+  // Does sub-tile st of the item hold allowed pairs for this wavefront's keys
+  // (band, bounds, block map)?  Both stages take the same decision, so stage
+  // B reads P exactly where stage A wrote it.  `full`: no pair of the
+  // sub-tile is outside the band or past Sq / Sk.
+  auto sub_live = [&](Item it, int st, int& mcode, bool& full) __attribute__((always_inline)) {
+    const int ia = it.qt * BQ + st * 32, ib = min(ia + 31, p.Sq - 1);
+    if (ia >= p.Sq || j0 >= p.Sk) return false;
+    const int jb = min(j0 + 31, p.Sk - 1);
+    if (j0 - ib > band.dhi || jb - ia < band.dlo) return false;  // nothing allowed
+    mcode = 1;
+    if constexpr (MASK) {
+      if (p.bmap) {
+        const int hq = hkv * p.G + it.gh;
+        const uint8_t code = p.bmap[b * p.bm_sb + hq * p.bm_sh + (int64_t)(ia / 32) * p.bm_cols + j0 / 64];
+        if (code == 2) return false;
+        mcode = code == 0 ? 0 : 1;
+      }
+    }
+    full = ia + 31 < p.Sq && j0 + 31 < p.Sk && jb - ia <= band.dhi && j0 - ib >= band.dlo;
+    return true;
   };
 
-  // ---- LDS operand reads of a Q / dO tile (rows swizzled with swz_kt)
-  // Row read (A operand of S / dP): query row qrow, head_dim chunk ds.
-  auto rowread = [&](const uint16_t* tile, int qrow, int ds) __attribute__((always_inline)) {
-    const int unit = (ds * 2 + g) ^ swz_kt<D>(qrow);
-    return *(const u32x4_t*)(tile + qrow * D + unit * 8);
-  };
-  // Transpose read (A operand of dV^T / dK^T): head_dim rows db*32 + l%32,
-  // the 8 queries of k-group g of k-step kk of sub-tile st (queries
-  // st*32 + kk*16 + {4g..4g+3, 8+4g..8+4g+3}, matching P's register rows).
-  const int tr_G = lane >> 4, tr_s = lane & 15, tr_g = tr_G >> 1, tr_dh = tr_G & 1;
-  auto trread = [&](const uint16_t* tile, int st, int db, int kk) __attribute__((always_inline)) {
-    const int u = db * 4 + tr_dh * 2 + ((tr_s & 3) >> 1);
-    const int half = (tr_s & 1) * 4;
-    const int row0 = st * 32 + kk * 16 + tr_g * 4 + (tr_s >> 2);
-    const int row1 = row0 + 8;
-    const s16x4_t lo4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row0 * D + (u ^ swz_kt<D>(row0)) * 8 + half));
-    const s16x4_t hi4 =
-        __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t*)(tile + row1 * D + (u ^ swz_kt<D>(row1)) * 8 + half));
-    const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo4), h2 = __builtin_bit_cast(u32x2_t, hi4);
-    return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
+  const TileReader<D> tr(lane);
+  // P of sub-tile st of P slot ps, k-step kk: the lane's 8 values, in the
+  // register layout both stages share
+  auto p_slot = [&](int ps, int st, int kk) __attribute__((always_inline)) {
+    return lds_p + ((ps * NG + kg) * NST + st) * 2 * 64 + kk * 64 + lane;
   };
 
-  // ---- one 32-query sub-tile against this wavefront's 32 keys
-  // `edge`: the sub-tile has pairs outside the band / past Sq or Sk.  It is a
-  // runtime flag, and only the masking of the scores branches on it: with the
-  // whole sub-tile instantiated twice, the two copies of the dK/dV MFMAs left
-  // the 128 accumulator registers in different places and every sub-tile
-  // paid 128 register moves at the join.
-  auto subtile = [&](bool edge, const uint16_t* qt_lds, const uint16_t* ot_lds, const float* l_lds,
-                     const float* d_lds, int st, int i0, int hq, float slope_l2, int mcode) __attribute__((always_inline)) {
-    // S = Q K^T, then dP = dO V^T: 2*DS MFMAs whose A operands (Q / dO row
-    // fragments) are read from LDS RPF MFMAs ahead; the sched_group_barriers
-    // keep the reads ahead of their MFMAs (one wavefront per SIMD: nothing
-    // else hides the LDS latency).
-    constexpr int NSD = 2 * DS, RPF = 6;
-    f32x16_t s = {}, dp = {};
+  // One stage: operand rows, the step loop, the epilogue.  Both stages run
+  // the same n_items + 1 steps and so the same barriers.
+  auto run = [&](auto stage_c) __attribute__((always_inline)) {
+    constexpr bool SB = decltype(stage_c)::value;  // stage B (dK)
+    u32x4_t br[DS];                                 // the lane's K row (stage A) or V row (stage B)
     {
-      auto aread = [&](int k) __attribute__((always_inline)) {
-        return k < DS ? rowread(qt_lds, st * 32 + r, k) : rowread(ot_lds, st * 32 + r, k - DS);
-      };
-      u32x4_t af[NSD];
+      const uint16_t* row = SB ? p.v + b * p.v_sb + hkv * p.v_sh + (int64_t)jc * p.v_ss
+                               : p.k + b * p.k_sb + hkv * p.k_sh + (int64_t)jc * p.k_ss;
 #pragma unroll
-      for (int k = 0; k < RPF; ++k) af[k] = aread(k);
+      for (int ds = 0; ds < DS; ++ds) br[ds] = *(const u32x4_t*)(row + ds * 16 + g * 8);
+    }
+    f32x16_t acc[DB];  // dV^T (stage A) or dK^T (stage B): lane row = key j, d = db*32 + vq*8 + 4g + e
 #pragma unroll
-      for (int k = 0; k < NSD; ++k) {
-        if (k + RPF < NSD) af[k + RPF] = aread(k + RPF);
-        if (k < DS) s = E::mfma(af[k], kr[k], s);
-        else dp = E::mfma(af[k], vr[k - DS], dp);
+    for (int db = 0; db < DB; ++db) acc[db] = (f32x16_t){};
+
+    // S (stage A: Q rows) or dP (stage B: dO rows) of sub-tile st: DS
+    // MFMAs whose A operands are read from LDS RPF MFMAs ahead, pinned with
+    // sched_group_barrier.
+    auto scores = [&](const uint16_t* rows, int st) __attribute__((always_inline)) {
+      f32x16_t s = {};
+      u32x4_t af[DS];
+#pragma unroll
+      for (int k = 0; k < RPF; ++k) af[k] = tr.row(rows, st, k);
+#pragma unroll
+      for (int k = 0; k < DS; ++k) {
+        if (k + RPF < DS) af[k + RPF] = tr.row(rows, st, k + RPF);
+        s = E::mfma(af[k], br[k], s);
       }
       __builtin_amdgcn_sched_group_barrier(0x100, RPF, 0);
 #pragma unroll
-      for (int k = 0; k < NSD; ++k) {
-        if (k + RPF < NSD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int k = 0; k < DS; ++k) {
+        if (k + RPF < DS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       }
-    }
-    // element v of the lane: query row st*32 + (v/4)*8 + 4g + v%4 of the tile
-    const char* mrow = nullptr;
-    if constexpr (MASK) {
-      if (mcode > 0) {
-        const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
-        mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)jc * p.mk_sj) * esz;
-      }
-    }
-    float x[16];
+      return s;
+    };
+    // The first TPF transpose operands of `grad`, read before the softmax /
+    // dZ VALU work so that their latency is hidden behind it.
+    auto tpre = [&](const uint16_t* tt, int st, u32x4_t* t0) __attribute__((always_inline)) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-      x[v] = s[v] * c;
-      if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - j);
-      if constexpr (MASK) {
-        if (mcode > 0 && i < p.Sq) x[v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)i * p.mk_si) * kLog2e;
-      }
-    }
-    if (edge) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        x[v] = qspan.ok(i) ? x[v] : -INFINITY;
-      }
-    }
-    float pv[16], dz[16];
-#pragma unroll
-    for (int vq = 0; vq < 4; ++vq) {
-      const f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
-      const f32x4_t d4 = *(const f32x4_t*)(d_lds + st * 32 + vq * 8 + g * 4);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int v = vq * 4 + e;
-        const float pe = __builtin_amdgcn_exp2f(x[v] - l4[e] * kLog2e);
-        pv[v] = pe;
-        dz[v] = pe * (dp[v] - d4[e]);
-      }
-    }
-    u32x4_t pb[2], zb[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      pb[kk] = (u32x4_t){E::pack(pv[kk * 8 + 0], pv[kk * 8 + 1]), E::pack(pv[kk * 8 + 2], pv[kk * 8 + 3]),
-                         E::pack(pv[kk * 8 + 4], pv[kk * 8 + 5]), E::pack(pv[kk * 8 + 6], pv[kk * 8 + 7])};
-      zb[kk] = (u32x4_t){E::pack(dz[kk * 8 + 0], dz[kk * 8 + 1]), E::pack(dz[kk * 8 + 2], dz[kk * 8 + 3]),
-                         E::pack(dz[kk * 8 + 4], dz[kk * 8 + 5]), E::pack(dz[kk * 8 + 6], dz[kk * 8 + 7])};
-    }
-    // dV^T += dO^T P and dK^T += Q^T dZ: 4*DB MFMAs, A operands from LDS
-    // transpose reads issued TPF MFMAs ahead.
-    {
-      constexpr int NTR = 4 * DB, TPF = 4;
-      auto tread = [&](int m) __attribute__((always_inline)) {
-        const int db = m / 4, kk = (m / 2) % 2;
-        return (m & 1) ? trread(qt_lds, st, db, kk) : trread(ot_lds, st, db, kk);
-      };
+      for (int m = 0; m < TPF; ++m) t0[m] = tr.tr(tt, st, m / 2, m % 2);
+    };
+    // acc^T += T^T X for sub-tile st: T = dO (stage A) or Q (stage B) through
+    // transpose reads, X = P or dZ from registers (k-step kk = m % 2).
+    auto grad = [&](const uint16_t* tt, int st, const u32x4_t* xb, const u32x4_t* t0) __attribute__((always_inline)) {
+      constexpr int NTR = 2 * DB;
       u32x4_t tf[NTR];
 #pragma unroll
-      for (int m = 0; m < TPF; ++m) tf[m] = tread(m);
+      for (int m = 0; m < TPF; ++m) tf[m] = t0[m];
 #pragma unroll
       for (int m = 0; m < NTR; ++m) {
-        if (m + TPF < NTR) tf[m + TPF] = tread(m + TPF);
-        const int db = m / 4, kk = (m / 2) % 2;
-        if (m & 1) dk[db] = E::mfma(tf[m], zb[kk], dk[db]);
-        else dv[db] = E::mfma(tf[m], pb[kk], dv[db]);
+        if (m + TPF < NTR) tf[m + TPF] = tr.tr(tt, st, (m + TPF) / 2, (m + TPF) % 2);
+        acc[m / 2] = E::mfma(tf[m], xb[m % 2], acc[m / 2]);
       }
-      __builtin_amdgcn_sched_group_barrier(0x100, 2 * TPF, 0);
 #pragma unroll
       for (int m = 0; m < NTR; ++m) {
         if (m + TPF < NTR) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       }
-    }
-  };
+    };
 
-  // ---- walk the q-heads of the group and the query tiles of the band
-  for (int gh = 0; gh < p.G; ++gh) {
-    const int hq = hkv * p.G + gh;
-    float slope_l2 = 0.f;
-    if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
-    if (nqt <= 0) break;
-    __syncthreads();  // the previous head's last tile is no longer read
-    load_tile(std::integral_constant<int, 0>{}, hq, qt_lo);
-    auto step = [&](auto slot_c, int qt) __attribute__((always_inline)) {
-      constexpr int SL = decltype(slot_c)::value;
-      __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies of tile qt landed
-      __syncthreads();                // ... and every wavefront's; tile qt-1 is no longer read
-      if (qt + 1 < qt_hi) load_tile(std::integral_constant<int, 1 - SL>{}, hq, qt + 1);
-      const uint16_t* qt_lds = SL ? lds_q1 : lds_q0;
-      const uint16_t* ot_lds = SL ? lds_o1 : lds_o0;
-      const float* l_lds = SL ? lds_l1 : lds_l0;
-      const float* d_lds = SL ? lds_d1 : lds_d0;
+    // element v of a lane's S / dP / P / dZ: query row st*32 + (v/4)*8 + 4g + v%4 of the item
+    auto stage_a = [&](Item it, auto sl_c, auto ps_c) __attribute__((always_inline)) {
+      constexpr int SL = decltype(sl_c)::value, PS = decltype(ps_c)::value;
+      const int hq = hkv * p.G + it.gh, i0 = it.qt * BQ;
+      float slope_l2 = 0.f;
+      if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
+      const uint16_t* qt_lds = lds_q + SL * TILE;
+      const uint16_t* ot_lds = lds_o + SL * TILE;
+      const float* l_lds = lds_l + SL * BQ;
 #pragma unroll
-      for (int st = 0; st < BQ / 32; ++st) {
-        const int i0 = qt * BQ;
-        const int ia = i0 + st * 32, ib = min(ia + 31, p.Sq - 1);
-        if (ia >= p.Sq || j0 >= p.Sk) continue;
-        // pairs (i in [ia, ib], j in [j0, j0+31]) with j - i in [dlo, dhi]
-        const int jb = min(j0 + 31, p.Sk - 1);
-        if (j0 - ib > band.dhi || jb - ia < band.dlo) continue;  // nothing allowed
-        int mcode = 1;
+      for (int st = 0; st < NST; ++st) {
+        int mcode;
+        bool full;
+        if (!sub_live(it, st, mcode, full)) continue;
+        const f32x16_t s = scores(qt_lds, st);
+        u32x4_t t0[TPF];
+        tpre(ot_lds, st, t0);
+        const char* mrow = nullptr;
         if constexpr (MASK) {
-          if (p.bmap) {
-            const uint8_t code = p.bmap[b * p.bm_sb + hq * p.bm_sh + (int64_t)(ia / 32) * p.bm_cols + j0 / 64];
-            if (code == 2) continue;
-            mcode = code == 0 ? 0 : 1;
+          if (mcode > 0) {
+            const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
+            mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)jc * p.mk_sj) * esz;
           }
         }
-        const bool full = ia + 31 < p.Sq && j0 + 31 < p.Sk && jb - ia <= band.dhi && j0 - ib >= band.dlo;
-        subtile(!full, qt_lds, ot_lds, l_lds, d_lds, st, i0, hq, slope_l2, mcode);
+        float x[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+          x[v] = s[v] * c;
+          if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - j);
+          if constexpr (MASK) {
+            if (mcode > 0 && i < p.Sq) x[v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)i * p.mk_si) * kLog2e;
+          }
+        }
+        if (!full) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+            x[v] = qspan.ok(i) ? x[v] : -INFINITY;
+          }
+        }
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - l4[e] * kLog2e);
+        }
+        u32x4_t pb[2];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          pb[kk] = (u32x4_t){E::pack(x[kk * 8 + 0], x[kk * 8 + 1]), E::pack(x[kk * 8 + 2], x[kk * 8 + 3]),
+                             E::pack(x[kk * 8 + 4], x[kk * 8 + 5]), E::pack(x[kk * 8 + 6], x[kk * 8 + 7])};
+          *p_slot(PS, st, kk) = pb[kk];
+        }
+        grad(ot_lds, st, pb, t0);
       }
     };
-    int qt = qt_lo;
-    for (; qt + 1 < qt_hi; qt += 2) {
-      step(std::integral_constant<int, 0>{}, qt);
-      step(std::integral_constant<int, 1>{}, qt + 1);
-    }
-    if (qt < qt_hi) step(std::integral_constant<int, 0>{}, qt);
-  }
 
-  // ---- epilogue: dK = scale * dZ^T Q, dV; lane row = key j, d = db*32 + vq*8 + 4g + e
-  if (j < p.Sk) {
-    uint16_t* dkrow = p.dk + b * p.dk_sb + hkv * p.dk_sh + (int64_t)j * p.dk_ss;
-    uint16_t* dvrow = p.dv + b * p.dv_sb + hkv * p.dv_sh + (int64_t)j * p.dv_ss;
+    auto stage_b = [&](Item it, auto sl_c, auto ps_c) __attribute__((always_inline)) {
+      constexpr int SL = decltype(sl_c)::value, PS = decltype(ps_c)::value;
+      const uint16_t* qt_lds = lds_q + SL * TILE;
+      const uint16_t* ot_lds = lds_o + SL * TILE;
+      const float* d_lds = lds_d + SL * BQ;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+      for (int st = 0; st < NST; ++st) {
+        int mcode;
+        bool full;
+        if (!sub_live(it, st, mcode, full)) continue;
+        const f32x16_t dp = scores(ot_lds, st);
+        u32x4_t t0[TPF];
+        tpre(qt_lds, st, t0);
+        u32x4_t zb[2];
 #pragma unroll
-      for (int vq = 0; vq < 4; ++vq) {
-        const int d0 = db * 32 + vq * 8 + g * 4;
-        *(u32x2_t*)(dkrow + d0) = (u32x2_t){E::pack(dk[db][vq * 4 + 0] * p.scale, dk[db][vq * 4 + 1] * p.scale),
-                                            E::pack(dk[db][vq * 4 + 2] * p.scale, dk[db][vq * 4 + 3] * p.scale)};
-        *(u32x2_t*)(dvrow + d0) = (u32x2_t){E::pack(dv[db][vq * 4 + 0], dv[db][vq * 4 + 1]),
-                                            E::pack(dv[db][vq * 4 + 2], dv[db][vq * 4 + 3])};
+        for (int kk = 0; kk < 2; ++kk) {
+          const u32x4_t pw = *p_slot(PS, st, kk);  // word w: elements kk*8 + 2w, kk*8 + 2w + 1
+          float z[8];
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int vq = kk * 2 + h;
+            const f32x4_t d4 = *(const f32x4_t*)(d_lds + st * 32 + vq * 8 + g * 4);
+            z[h * 4 + 0] = E::lo(pw[h * 2 + 0]) * (dp[vq * 4 + 0] - d4[0]);
+            z[h * 4 + 1] = E::hi(pw[h * 2 + 0]) * (dp[vq * 4 + 1] - d4[1]);
+            z[h * 4 + 2] = E::lo(pw[h * 2 + 1]) * (dp[vq * 4 + 2] - d4[2]);
+            z[h * 4 + 3] = E::hi(pw[h * 2 + 1]) * (dp[vq * 4 + 3] - d4[3]);
+          }
+          zb[kk] = (u32x4_t){E::pack(z[0], z[1]), E::pack(z[2], z[3]), E::pack(z[4], z[5]), E::pack(z[6], z[7])};
+        }
+        grad(qt_lds, st, zb, t0);
       }
-  }
+    };
+
+    // Step s: stage A on item s (Q/dO slot s%3, P slot s%2), stage B on item
+    // s - 1, item s + 1 loading into slot (s+1)%3.  The barrier at the top of
+    // step s is where item s has landed, P of item s-1 is written, and slot
+    // (s+1)%3 (last read in step s-1 by stage B) and P slot s%2 are free.
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    if (n_items > 0) load_item(Item{0, qt_lo}, I0{});
+    Item ia{0, qt_lo}, ib{0, qt_lo};
+    auto step = [&](auto sa_c, auto pa_c, int s) __attribute__((always_inline)) {
+      constexpr int SA = decltype(sa_c)::value, PA = decltype(pa_c)::value;
+      __builtin_amdgcn_s_waitcnt(0);  // this wavefront's copies and P writes landed
+      __syncthreads();                // ... and every wavefront's
+      const Item in = next_item(ia);
+      if (s + 1 < n_items) load_item(in, std::integral_constant<int, (SA + 1) % NSL>{});
+      if constexpr (!SB) {
+        if (s < n_items) stage_a(ia, sa_c, pa_c);
+      } else {
+        if (s > 0) stage_b(ib, std::integral_constant<int, (SA + NSL - 1) % NSL>{}, std::integral_constant<int, 1 - PA>{});
+      }
+      ib = ia;
+      ia = in;
+    };
+    for (int s = 0; s <= n_items; s += 6) {
+      step(I0{}, I0{}, s);
+      if (s + 1 <= n_items) step(I1{}, I1{}, s + 1);
+      if (s + 2 <= n_items) step(I2{}, I0{}, s + 2);
+      if (s + 3 <= n_items) step(I0{}, I1{}, s + 3);
+      if (s + 4 <= n_items) step(I1{}, I0{}, s + 4);
+      if (s + 5 <= n_items) step(I2{}, I1{}, s + 5);
+    }
+
+    // ---- epilogue: dV, or dK = scale * dZ^T Q
+    if (j < p.Sk) {
+      uint16_t* row = SB ? p.dk + b * p.dk_sb + hkv * p.dk_sh + (int64_t)j * p.dk_ss
+                         : p.dv + b * p.dv_sb + hkv * p.dv_sh + (int64_t)j * p.dv_ss;
+      const float f = SB ? p.scale : 1.f;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int d0 = db * 32 + vq * 8 + g * 4;
+          *(u32x2_t*)(row + d0) = (u32x2_t){E::pack(acc[db][vq * 4 + 0] * f, acc[db][vq * 4 + 1] * f),
+                                            E::pack(acc[db][vq * 4 + 2] * f, acc[db][vq * 4 + 3] * f)};
+        }
+    }
+  };
+  if (wave >= NG) run(std::true_type{});
+  else run(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------
@@ -639,11 +685,12 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
 // Launch of both gradient kernels for one (dtype, D); feat = kFeatAlibi | kFeatMask.
 template <class E, int D>
 hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
-  const dim3 g_kv((unsigned)(p.B * p.Hkv * p.num_kblk)), g_q((unsigned)(p.B * p.Hq * p.num_mblk)), blk(256);
+  const dim3 g_kv((unsigned)(p.B * p.Hkv * p.num_kblk)), g_q((unsigned)(p.B * p.Hq * p.num_mblk)), blk(256),
+      blk_kv(512);
   switch (feat & 3) {
 #define TRINIX_BWD_CASE(F)                                                                                        \
   case F:                                                                                                         \
-    hipLaunchKernelGGL((attn_bwd_dkdv<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_kv, blk, 0, st, p); \
+    hipLaunchKernelGGL((attn_bwd_dkdv<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_kv, blk_kv, 0, st, p); \
     hipLaunchKernelGGL((attn_bwd_dq<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_q, blk, 0, st, p);    \
     return hipGetLastError();
     TRINIX_BWD_CASE(0)
