@@ -58,6 +58,12 @@ CASES = [
     (2, 96, 150, 2, 2, 64, torch.bfloat16, dict(softmax_scale=0.2)),
     (1, 130, 130, 4, 2, 64, torch.float16, dict(window_size=(20, 33))),
     (2, 128, 128, 4, 4, 64, torch.float16, dict(alibi_slopes=orc.alibi_slopes(4))),
+    # the dK/dV kernel pipelines (q-head, 64-query tile) items over two
+    # stages: one item (the second stage runs alone on the last step), two
+    # items, and a key block past Sk with a single query tile
+    (1, 17, 17, 1, 1, 128, torch.float16, dict(causal=True)),
+    (1, 40, 70, 2, 1, 64, torch.bfloat16, dict()),
+    (2, 64, 200, 3, 1, 128, torch.bfloat16, dict(window_size=(0, 90))),
 ]
 
 
