@@ -295,7 +295,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
       return s;
     };
     // The first TPF transpose operands of `grad`, read before the softmax /
-    // dZ VALU work so that their latency is hidden behind it.
+    // dZ VALU work so that their latency is hidden behind it.  The MFMA
+    // phases run at wave priority 1 and the VALU phases at 0, so the SIMD
+    // favours issuing the MFMAs of one stage while the other does VALU work.
     auto tpre = [&](const uint16_t* tt, int st, u32x4_t* t0) __attribute__((always_inline)) {
 #pragma unroll
       for (int m = 0; m < TPF; ++m) t0[m] = tr.tr(tt, st, m / 2, m % 2);
@@ -333,9 +335,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         int mcode;
         bool full;
         if (!sub_live(it, st, mcode, full)) continue;
+        __builtin_amdgcn_s_setprio(1);
         const f32x16_t s = scores(qt_lds, st);
         u32x4_t t0[TPF];
         tpre(ot_lds, st, t0);
+        __builtin_amdgcn_s_setprio(0);
         const char* mrow = nullptr;
         if constexpr (MASK) {
           if (mcode > 0) {
@@ -373,7 +377,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
                              E::pack(x[kk * 8 + 4], x[kk * 8 + 5]), E::pack(x[kk * 8 + 6], x[kk * 8 + 7])};
           *p_slot(PS, st, kk) = pb[kk];
         }
+        __builtin_amdgcn_s_setprio(1);
         grad(ot_lds, st, pb, t0);
+        __builtin_amdgcn_s_setprio(0);
       }
     };
 
@@ -387,9 +393,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         int mcode;
         bool full;
         if (!sub_live(it, st, mcode, full)) continue;
+        __builtin_amdgcn_s_setprio(1);
         const f32x16_t dp = scores(ot_lds, st);
         u32x4_t t0[TPF];
         tpre(qt_lds, st, t0);
+        __builtin_amdgcn_s_setprio(0);
         u32x4_t zb[2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
@@ -406,7 +414,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
           }
           zb[kk] = (u32x4_t){E::pack(z[0], z[1]), E::pack(z[2], z[3]), E::pack(z[4], z[5]), E::pack(z[6], z[7])};
         }
+        __builtin_amdgcn_s_setprio(1);
         grad(qt_lds, st, zb, t0);
+        __builtin_amdgcn_s_setprio(0);
       }
     };
 
