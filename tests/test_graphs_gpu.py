@@ -64,6 +64,25 @@ def test_graph_prefill_gqa_fused_rope():
     replay_and_check(g, out, [q, k, v], fn)
 
 
+def test_graph_alibi_block_mask_with_blockmap_prepass():
+    # the mask path launches the block-map pre-pass and then the attention
+    # kernel; the mask itself is a static input too
+    B, S, H, D = 2, 320, 4, 64
+    q = torch.zeros(B, S, H, D, device=DEV, dtype=torch.float16)
+    k = torch.zeros(B, S, H, D, device=DEV, dtype=torch.float16)
+    v = torch.zeros(B, S, H, D, device=DEV, dtype=torch.float16)
+    mask = torch.zeros(S, S, device=DEV)
+    mask[64:128, 128:192] = float("-inf")
+    mask[200:260, :40] = float("-inf")
+    slopes = torch.tensor([2.0 ** (-2 * (h + 1)) for h in range(H)], device=DEV)
+
+    def fn():
+        return triton_attn_func(q, k, v, attn_mask=mask, alibi_slopes=slopes)
+
+    g, out = capture(fn)
+    replay_and_check(g, out, [q, k, v], fn)
+
+
 def test_graph_decode_split_kv_with_lse():
     B, Sk, H, HKV, D = 2, 3000, 16, 4, 128
     q = torch.zeros(B, 1, H, D, device=DEV, dtype=torch.bfloat16)
