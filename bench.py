@@ -279,9 +279,11 @@ def decode_measure(torch, iters=30):
 def layer_measure(torch, iters=10):
     """The C3 model's attention layer forward (Llama-3-8B GQA: E=4096, 32 q /
     8 kv heads, RoPE 5e5, causal, qk_norm=True, B=1, S=8192, bf16, inference)
-    with the fused RoPE + qk RMSNorm kernel and with the eager norm modules,
-    plus that kernel alone on q (algorithmic bytes: q read and written once).
-    The projections are torch Linear layers (hipBLASLt GEMMs)."""
+    three ways: q's RoPE + RMSNorm in the attention prologue and k's in the
+    fused RoPE + qk RMSNorm kernel (the default); both through that kernel;
+    the eager norm modules.  Plus that kernel alone on q (algorithmic bytes:
+    q read and written once).  The projections are torch Linear layers
+    (hipBLASLt GEMMs)."""
     import trinix_amd as tx
     from trinix_amd.kernels import qk_rmsnorm
 
@@ -290,17 +292,18 @@ def layer_measure(torch, iters=10):
                      "qk_norm (RMSNorm), bf16, no grad"}
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn(B, S, H * D, device="cuda", generator=g).to(torch.bfloat16)
-    for fused in (True, False):
+    for mode in ("us_fused_qk_norm", "us_fused_qk_norm_q_separate", "us_eager_qk_norm"):
+        fused = mode != "us_eager_qk_norm"
         layer = tx.FastGroupedQueryAttention(H * D, H, HKV, causal=True, position_method="rope", rope_base=500000.0,
                                              qk_norm=True, max_seq_len=S).to("cuda", torch.bfloat16)
         if not fused:
             layer._fused_qk_norm_applies = lambda q, k: False
+        layer.fuse_q_norm_in_attention = mode == "us_fused_qk_norm"
         with torch.no_grad():
             for _ in range(3):
                 layer(x)
-            res["us_fused_qk_norm" if fused else "us_eager_qk_norm"] = round(
-                time_events(lambda: layer(x), iters, torch) * 1e3, 1)
-        if fused:
+            res[mode] = round(time_events(lambda: layer(x), iters, torch) * 1e3, 1)
+        if mode == "us_fused_qk_norm":
             q = torch.randn(B, S, H, D, device="cuda", generator=g).to(torch.bfloat16)
             cos, sin = layer.position_embedding(q, S)
             w = layer.q_norm.weight.detach()

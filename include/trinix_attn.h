@@ -54,7 +54,7 @@
 extern "C" {
 #endif
 
-#define TRINIX_ATTN_ABI_VERSION 1
+#define TRINIX_ATTN_ABI_VERSION 2
 
 typedef enum trinix_status {
   TRINIX_OK = 0,
@@ -117,6 +117,15 @@ typedef struct trinix_attn_fwd_args {
   const void* rope_cos;         /* fused RoPE on q: cos/sin rows indexed by the  */
   const void* rope_sin;         /* query position, first D/2 columns used; dtype */
   int64_t rope_stride;          /* of q; NULL = no fused RoPE                    */
+  /* Fused qk-norm of q (the layers' q RMSNorm over head_dim after RoPE,
+   * reference trinix/layers/attention/grouped_query_attention.py:167-177):
+   * each q row, after the fused RoPE if any, becomes
+   * weight * dtype(h * rsqrt(mean(h^2) + eps)), with the rounding of
+   * trinix_qk_norm, so q is bitwise the one trinix_qk_norm would write.
+   * head_dim weights in q's dtype, 16-byte aligned; bf16/fp16 only, not
+   * with a mask or dropout (TRINIX_ERR_BAD_ARGUMENT); NULL = none. */
+  const void* q_norm_weight;
+  float q_norm_eps;
 } trinix_attn_fwd_args;
 
 /* Attention forward on `stream`. */
@@ -131,7 +140,8 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* args, void* stream);
  * log-sum-exp.
  *
  * trinix_attn_fwd_splitkv_plan: *num_splits = 0 if the split-KV kernel does
- * not apply (fp32, dropout, fused RoPE, seqlen_q > 16, no visible key): use
+ * not apply (fp32, dropout, fused RoPE or q norm, seqlen_q > 16, no visible
+ * key): use
  * trinix_attn_fwd.  Otherwise the chunk count and the size of the fp32
  * workspace trinix_attn_fwd_splitkv needs (0 for a single chunk).  Host
  * only, no launch.

@@ -107,3 +107,67 @@ def test_qk_norm_layer_training_keeps_eager_gradients():
     out.float().sum().backward()
     assert layer.q_norm.weight.grad is not None and layer.k_norm.weight.grad is not None
     assert torch.isfinite(x.grad).all()
+
+
+def _rope_tables(q, S):
+    emb = tx.FastRoPEPositionEmbedding(q.shape[-1], max_position_embeddings=S, base=500000.0).to(DEV)
+    return emb(q, S)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("Sq", [150, 8])
+def test_q_norm_fused_into_attention_is_bitwise_the_two_kernel_path(D, dtype, rope, Sq, monkeypatch):
+    """q's RoPE + RMSNorm in the attention kernel's prologue gives the
+    output of qk_rmsnorm followed by the attention kernel, bit for bit (the
+    prologue repeats qk_rmsnorm's rounding and its sum-of-squares order)."""
+    from trinix_amd.kernels import TritonAttentionKernel, rope_apply
+    from trinix_amd.kernels import attention_kernel as ak
+
+    monkeypatch.setattr(ak, "SPLITKV_ENABLED", False)  # short q: the same prefill kernel on both sides
+    if D == 64:  # small D=64 grids take the key split, which the fused norm is not built with
+        monkeypatch.setenv("TRINIX_ATTN_CFG", "4,2,64,1")
+    g = torch.Generator().manual_seed(D + Sq + (7 if rope else 0))
+    B, Sk, H, HKV = 2, 150, 4, 2
+    q = (torch.randn(B, Sq, H, D, generator=g) * 3).to(DEV, dtype)
+    k = torch.randn(B, Sk, HKV, D, generator=g).to(DEV, dtype)
+    v = torch.randn(B, Sk, HKV, D, generator=g).to(DEV, dtype)
+    w = (torch.rand(D, generator=g) + 0.5).to(DEV, dtype)
+    eps = 1e-5
+    kw = {}
+    cos = sin = None
+    if rope:
+        cos, sin = _rope_tables(q, max(Sq, Sk))
+        k = rope_apply(k, cos, sin)
+        kw = dict(rotary_cos=cos, rotary_sin=sin, rotary_k=False)
+    ref = TritonAttentionKernel.apply(qk_rmsnorm(q, w, eps, cos, sin), k, v, causal=True)
+    out = TritonAttentionKernel.apply(q, k, v, causal=True, q_norm_weight=w, q_norm_eps=eps, **kw)
+    assert torch.equal(out, ref)
+
+
+def test_q_norm_fused_argument_errors():
+    from trinix_amd.kernels import TritonAttentionKernel
+    from trinix_amd.kernels.attention_kernel import attention
+
+    q = torch.randn(1, 32, 2, 128, device=DEV, dtype=torch.bfloat16)
+    w = torch.ones(128, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        TritonAttentionKernel.apply(q.float(), q.float(), q.float(), q_norm_weight=w.float())
+    with pytest.raises(ValueError):
+        TritonAttentionKernel.apply(q, q, q, q_norm_weight=w[:64])
+    q96 = torch.randn(1, 32, 2, 96, device=DEV, dtype=torch.bfloat16)  # padded to 128: no fused norm
+    with pytest.raises(ValueError):
+        TritonAttentionKernel.apply(q96, q96, q96, q_norm_weight=torch.ones(96, device=DEV, dtype=torch.bfloat16))
+    qg = q.clone().requires_grad_(True)
+    with pytest.raises(ValueError):
+        attention(qg, q, q, q_norm_weight=w)
+    with pytest.raises(ValueError):  # built without the mask and dropout kernels
+        TritonAttentionKernel.apply(q, q, q, attn_mask=torch.zeros(32, 32, device=DEV), q_norm_weight=w)
+    with pytest.raises(ValueError):
+        TritonAttentionKernel.apply(q, q, q, dropout_p=0.1, q_norm_weight=w)
+    # ALiBi is built with the fused norm: same output as the two-kernel path
+    slopes = torch.tensor([0.25, 0.0625], device=DEV)
+    ref = TritonAttentionKernel.apply(qk_rmsnorm(q, w, 1e-6), q, q, causal=True, alibi_slopes=slopes)
+    out = TritonAttentionKernel.apply(q, q, q, causal=True, alibi_slopes=slopes, q_norm_weight=w, q_norm_eps=1e-6)
+    assert torch.equal(out, ref)

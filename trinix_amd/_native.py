@@ -34,7 +34,7 @@ TRINIX_U8 = 3
 BLOCKMAP_ROWS = 32
 BLOCKMAP_COLS = 64
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 Int64x4 = c_int64 * 4
 Int64x2 = c_int64 * 2
@@ -78,6 +78,8 @@ class AttnFwdArgs(ctypes.Structure):
         ("rope_cos", c_void_p),
         ("rope_sin", c_void_p),
         ("rope_stride", c_int64),
+        ("q_norm_weight", c_void_p),
+        ("q_norm_eps", c_float),
     ]
 
 

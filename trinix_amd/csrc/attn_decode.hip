@@ -387,7 +387,7 @@ struct SplitPlan {
 
 bool make_split_plan(const trinix_attn_fwd_args* a, SplitPlan* pl) {
   if (a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F16) return false;
-  if (a->dropout_p > 0.f || a->rope_cos) return false;
+  if (a->dropout_p > 0.f || a->rope_cos || a->q_norm_weight) return false;
   if (a->seqlen_q > kDecodeMaxSq) return false;
   if (a->head_dim != 64 && a->head_dim != 128) return false;
   const int64_t Sq = a->seqlen_q, Sk = a->seqlen_k;

@@ -328,6 +328,12 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (a->rope_cos && esize == 2 &&
       (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
     return TRINIX_ERR_BAD_STRIDE;
+  if (a->q_norm_weight) {
+    if (esize != 2) return TRINIX_ERR_BAD_DTYPE;
+    if (a->mask || a->dropout_p > 0.f) return TRINIX_ERR_BAD_ARGUMENT;
+    if (!aligned16(a->q_norm_weight)) return TRINIX_ERR_BAD_STRIDE;
+    if (!(a->q_norm_eps >= 0.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  }
 
   return TRINIX_OK;
 }
@@ -406,7 +412,8 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.Hkv = (int)a->nheads_kv;
   p.G = p.Hq / p.Hkv;
   const bool f32 = a->dtype == TRINIX_F32;
-  const Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q);
+  Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q);
+  if (a->q_norm_weight) cfg.ks = 1;  // the fused q RMSNorm is built without the key split
   const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw / cfg.ks;
   p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
   const int64_t total = (int64_t)p.B * p.Hq * p.num_mblk;
@@ -440,6 +447,8 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.rope_cos = (const uint16_t*)a->rope_cos;
   p.rope_sin = (const uint16_t*)a->rope_sin;
   p.rope_stride = a->rope_stride;
+  p.qn_w = (const uint16_t*)a->q_norm_weight;
+  p.qn_eps = a->q_norm_eps;
 
   hipStream_t st = (hipStream_t)stream;
   (void)hipGetLastError();
@@ -451,7 +460,8 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
     else hipLaunchKernelGGL((attn_fwd_f32<256, kWavesF32>), grid, block, 0, st, p);
     err = hipGetLastError();
   } else {
-    const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0);
+    const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0) |
+                     (p.qn_w ? kFeatQNorm : 0);
     const bool bf = a->dtype == TRINIX_BF16;
     if (a->head_dim == 64)
       err = bf ? launch_attn16_bf16_d64(p, cfg, feat, st) : launch_attn16_f16_d64(p, cfg, feat, st);

@@ -42,7 +42,7 @@
 
 namespace trinix {
 
-template <class E, int D, int BN, int NW, int OCC, int KS, bool ALIBI, bool MASK, bool DROP>
+template <class E, int D, int BN, int NW, int OCC, int KS, bool ALIBI, bool MASK, bool DROP, bool QN>
 __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
   // KS = 2 splits each 32-row group's keys between two wavefronts: wavefront
   // 2r + kp owns rows 32r..32r+31 and the tiles t_lo + KS*s + kp; the halves
@@ -180,6 +180,53 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
         }
         qr[ds] = x1;
         qr[ds + DS / 2] = x2;
+      }
+    }
+    if constexpr (QN) {
+#pragma clang fp contract(off)
+      // Fused qk-norm (RMSNorm over head_dim after RoPE, reference
+      // trinix/layers/attention/grouped_query_attention.py:167-177) with
+      // trinix_qk_norm's arithmetic, so q is bitwise the q it writes.  There,
+      // lane c of a row sums chunks c and c + DS (8 elements each) and a
+      // shuffle tree adds c^1, c^2, c^4, ...  Here chunk k of this lane is
+      // chunk c = 2k + g: c^1 is the same k in the other half-wave, c^2m is
+      // chunk k^m of this lane.  IEEE addition is commutative, so every
+      // pairing adds the same two values and all lanes end with one sum.
+      constexpr int NH = DS / 2;
+      float part[NH];
+#pragma unroll
+      for (int k = 0; k < NH; ++k) {
+        float ssq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float y1 = (e & 1) ? E::hi(qr[k][e / 2]) : E::lo(qr[k][e / 2]);
+          const float y2 = (e & 1) ? E::hi(qr[k + NH][e / 2]) : E::lo(qr[k + NH][e / 2]);
+          ssq += y1 * y1 + y2 * y2;
+        }
+        part[k] = ssq;
+      }
+#pragma unroll
+      for (int k = 0; k < NH; ++k) part[k] += __shfl_xor(part[k], 32);
+#pragma unroll
+      for (int m = 1; m < NH; m <<= 1) {
+        float nxt[NH];
+#pragma unroll
+        for (int k = 0; k < NH; ++k) nxt[k] = part[k] + part[k ^ m];
+#pragma unroll
+        for (int k = 0; k < NH; ++k) part[k] = nxt[k];
+      }
+      // mean(h^2): D is a power of two, so sum / D is exact scaling
+      const float rn = rsqrtf(part[0] / (float)D + p.qn_eps);
+#pragma unroll
+      for (int ds = 0; ds < DS; ++ds) {
+        const u32x4_t ww = *(const u32x4_t*)(p.qn_w + ds * 16 + g * 8);
+        u32x4_t x = qr[ds];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float n0 = round_to<E>(E::lo(x[e]) * rn), n1 = round_to<E>(E::hi(x[e]) * rn);
+          x[e] = E::pack(E::lo(ww[e]) * n0, E::hi(ww[e]) * n1);
+        }
+        qr[ds] = x;
       }
     }
     if (q_neg)
@@ -639,7 +686,7 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
     hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,     \
-                                        (F & kFeatDropout) != 0>),                                              \
+                                        (F & kFeatDropout) != 0, (F & kFeatQNorm) != 0>),                       \
                        grid, block, 0, st, p);                                                                  \
     return hipGetLastError();
     TRINIX_CASE(0)
@@ -650,9 +697,22 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
     TRINIX_CASE(5)
     TRINIX_CASE(6)
     TRINIX_CASE(7)
-#undef TRINIX_CASE
-    default: return hipErrorInvalidValue;
+    default:
+      break;
   }
+  // The fused q RMSNorm is its own instantiation (the other kernels keep
+  // their code unchanged): without and with ALiBi, one wavefront per row
+  // group; the host rejects it with a mask or dropout.
+  if constexpr (KS == 1) {
+    switch (feat) {
+      TRINIX_CASE((kFeatQNorm))
+      TRINIX_CASE((kFeatQNorm | kFeatAlibi))
+      default:
+        break;
+    }
+  }
+#undef TRINIX_CASE
+  return hipErrorInvalidValue;
 }
 
 // Tile configs built per (dtype, D), every feature combination:

@@ -36,6 +36,8 @@ struct FwdParams {
   const uint16_t* rope_cos;
   const uint16_t* rope_sin;
   int64_t rope_stride;
+  const uint16_t* qn_w;  // fused q RMSNorm weight (head_dim), or null
+  float qn_eps;
 };
 
 // Tile shape of one 16-bit kernel instantiation.
@@ -119,6 +121,6 @@ hipError_t launch_attn16_f16_d256(const FwdParams& p, Cfg16 cfg, int feat, hipSt
 int validate_fwd_args(const trinix_attn_fwd_args* a);
 
 // Feature bits of a launch (compile-time flags of the 16-bit kernels).
-enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4 };
+enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4, kFeatQNorm = 8 };
 
 }  // namespace trinix

@@ -179,6 +179,8 @@ class TritonAttentionKernel:
         rotary_k: bool = True,
         return_lse: bool = False,
         use_blockmap: bool = True,
+        q_norm_weight: Optional[torch.Tensor] = None,
+        q_norm_eps: float = 1e-6,
     ):
         """Attention forward (reference ``attention_kernel.py:497-664``); the
         output carries no autograd history, as in the reference.
@@ -187,17 +189,21 @@ class TritonAttentionKernel:
         reference RoPE tables in ``q.dtype``, indexed by position) apply RoPE
         to q inside the kernel and to k by a pre-pass (``rotary_k=False``
         leaves k as given); ``return_lse`` also returns the (B, H, Sq) fp32
-        log-sum-exp.  ``attention()`` is the differentiable entry point.
+        log-sum-exp; ``q_norm_weight``/``q_norm_eps`` apply the layers' q
+        RMSNorm over head_dim (after the fused RoPE) in the kernel's q
+        prologue, bitwise as ``qk_rmsnorm`` would (bf16/fp16, head_dim 64,
+        128 or 256).  ``attention()`` is the differentiable entry point.
         """
         out, lse, _ = _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes,
-                               rotary_cos, rotary_sin, rotary_k, return_lse, use_blockmap)
+                               rotary_cos, rotary_sin, rotary_k, return_lse, use_blockmap,
+                               q_norm_weight=q_norm_weight, q_norm_eps=q_norm_eps)
         if return_lse:
             return out, lse
         return out
 
 
 def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, rotary_cos, rotary_sin,
-             rotary_k, return_lse, use_blockmap, keep_state=False):
+             rotary_k, return_lse, use_blockmap, keep_state=False, q_norm_weight=None, q_norm_eps=1e-6):
     """Launch ``trinix_attn_fwd``; returns (out, lse or None, state).  With
     ``keep_state`` the prepared operands (padded, strided as the kernel reads
     them), the lse and the mask / slope tensors are kept for the backward."""
@@ -220,6 +226,15 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
         raise ValueError(f"head_dim {D} > {KERNEL_HEAD_DIMS[-1]} is not supported")
     if not (0.0 <= dropout_p < 1.0):
         raise ValueError(f"dropout_p must be in [0, 1), got {dropout_p}")
+    if q_norm_weight is not None:
+        if q.dtype == torch.float32:
+            raise ValueError("the fused q RMSNorm runs in bf16/fp16")
+        if d_kernel != D:
+            raise ValueError(f"the fused q RMSNorm needs head_dim in {KERNEL_HEAD_DIMS}, got {D}")
+        if tuple(q_norm_weight.shape) != (D,):
+            raise ValueError(f"q_norm_weight must have shape ({D},), got {tuple(q_norm_weight.shape)}")
+        if attn_mask is not None or dropout_p > 0.0:
+            raise ValueError("the fused q RMSNorm runs without a mask or dropout")
     if scale is None:
         scale = D ** -0.5
     device = q.device
@@ -246,7 +261,7 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
     # Decode-shaped calls (few query rows, long KV) take the split-KV kernel;
     # it has no fused RoPE, so q is rotated here first.
     split_kv = (SPLITKV_ENABLED and Sq <= SPLITKV_MAX_SQ and q.dtype != torch.float32 and dropout_p == 0.0
-                and d_kernel <= 128)
+                and d_kernel <= 128 and q_norm_weight is None)
     if split_kv and rotary_cos is not None:
         from .rope_kernel import rope_apply
         q = rope_apply(q, rotary_cos, rotary_sin)
@@ -325,6 +340,13 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
                 cos = cos.contiguous()
         keep += [cos, sin]
         args.rope_cos, args.rope_sin, args.rope_stride = cos.data_ptr(), sin.data_ptr(), cos.stride(0)
+
+    if q_norm_weight is not None:
+        qw = q_norm_weight.detach().to(device=device, dtype=q.dtype)
+        if not qw.is_contiguous() or qw.data_ptr() % 16:
+            qw = qw.contiguous()
+        keep.append(qw)
+        args.q_norm_weight, args.q_norm_eps = qw.data_ptr(), float(q_norm_eps)
 
     launched = False
     if split_kv:
@@ -428,7 +450,8 @@ _warned_no_grad = set()
 
 
 def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, window_size=None, alibi_slopes=None,
-              *, rotary_cos=None, rotary_sin=None, rotary_k=True, return_lse=False):
+              *, rotary_cos=None, rotary_sin=None, rotary_k=True, return_lse=False, q_norm_weight=None,
+              q_norm_eps=1e-6):
     """Attention with gradients when q, k or v require them (bf16/fp16, no
     dropout, head_dim <= 128); otherwise ``TritonAttentionKernel.apply``.
 
@@ -439,6 +462,8 @@ def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, 
     required keep the reference's behaviour, a detached output, and warn once.
     """
     needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
+    if q_norm_weight is not None and (needs_grad or (torch.is_grad_enabled() and q_norm_weight.requires_grad)):
+        raise ValueError("the fused q RMSNorm has no backward: apply the norm module before attention() to train")
     if needs_grad:
         dk = kernel_head_dim(q.shape[-1])
         if q.dtype in (torch.float16, torch.bfloat16) and dropout_p == 0.0 and dk in BACKWARD_HEAD_DIMS:
@@ -454,7 +479,8 @@ def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, 
                           "Triton path", stacklevel=2)
     return TritonAttentionKernel.apply(q, k, v, attn_mask=attn_mask, causal=causal, scale=scale, dropout_p=dropout_p,
                                        window_size=window_size, alibi_slopes=alibi_slopes, rotary_cos=rotary_cos,
-                                       rotary_sin=rotary_sin, rotary_k=rotary_k, return_lse=return_lse)
+                                       rotary_sin=rotary_sin, rotary_k=rotary_k, return_lse=return_lse,
+                                       q_norm_weight=q_norm_weight, q_norm_eps=q_norm_eps)
 
 
 def attention_flops(batch: int, nheads: int, seqlen_q: int, seqlen_k: int, head_dim: int,

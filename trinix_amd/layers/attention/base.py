@@ -72,7 +72,13 @@ class FastBaseAttention(nn.Module):
     use_sliding_window=False, sliding_window_size=None, qk_norm=False,
     qk_norm_type='rmsnorm', use_triton_norm=True, use_triton_embeddings=True,
     add_zero_attn=False.
+
+    ``fuse_q_norm_in_attention`` (class attribute, default True): with the
+    fused qk RMSNorm in inference, q's RoPE and norm run in the attention
+    kernel's prologue (bitwise the same q) instead of their own pass.
     """
+
+    fuse_q_norm_in_attention = True
 
     def __init__(
         self,
@@ -266,13 +272,15 @@ class FastBaseAttention(nn.Module):
         out = torch.bmm(w, vh)
         return out.reshape(batch_size, num_heads, seq_len, head_dim).transpose(1, 2)
 
-    def _apply_triton_attention(self, q, k, v, attn_mask=None, rotary=None):
+    def _apply_triton_attention(self, q, k, v, attn_mask=None, rotary=None, q_norm=None):
         """HIP kernel backend (reference base.py:402-439), no fallback."""
         if not TritonAttentionKernel.is_available():
             raise RuntimeError("HIP attention kernel not available (build trinix_amd; needs a gfx950 GPU)")
         kw = {}
         if rotary is not None:
             kw = dict(rotary_cos=rotary[0], rotary_sin=rotary[1], rotary_k=False)
+        if q_norm is not None:
+            kw.update(q_norm_weight=q_norm.weight, q_norm_eps=q_norm.eps)
         return attention(
             q, k, v, attn_mask=attn_mask, causal=self.causal, scale=self.scale,
             dropout_p=self.dropout if self.training else 0.0, window_size=self._window_size(),
@@ -315,6 +323,12 @@ class FastBaseAttention(nn.Module):
                      and self._uses_kernel(q) and position_ids is None and not self.qk_norm
                      and past_key_value is None and not (use_zero_attn and self.add_zero_attn))
         fuse_norm = self._fused_qk_norm_applies(q, k)
+        # q's RoPE + RMSNorm in the attention kernel's prologue (positions are
+        # the query rows: no position_ids, no cache, no zero-attention row;
+        # that kernel takes no mask and no dropout)
+        fuse_qnorm = (self.fuse_q_norm_in_attention and fuse_norm and position_ids is None and past_key_value is None
+                      and not (use_zero_attn and self.add_zero_attn) and q.shape[-1] in (64, 128, 256)
+                      and attention_mask is None and not (self.training and self.dropout > 0.0))
         if fuse_rope:
             # q is rotated inside the attention kernel; k by the RoPE kernel
             # (it is also the returned cache).
@@ -331,7 +345,10 @@ class FastBaseAttention(nn.Module):
             cos = sin = None
             if self.position_method == "rope" and self.position_embedding is not None:
                 cos, sin = self.position_embedding(q, max(seq_len_q, seq_len_k))
-            q = qk_rmsnorm(q, self.q_norm.weight, self.q_norm.eps, cos, sin, position_ids)
+            if fuse_qnorm:
+                rotary = (cos, sin) if cos is not None else None
+            else:
+                q = qk_rmsnorm(q, self.q_norm.weight, self.q_norm.eps, cos, sin, position_ids)
             k = qk_rmsnorm(k, self.k_norm.weight, self.k_norm.eps, cos, sin, position_ids)
             attention_mask = self._merge_position_bias(attention_mask, None)
         else:
@@ -354,7 +371,7 @@ class FastBaseAttention(nn.Module):
         k = k.transpose(1, 2)
         v = v.transpose(1, 2)
         if self._uses_kernel(q):
-            out = self._apply_triton_attention(q, k, v, attention_mask, rotary)
+            out = self._apply_triton_attention(q, k, v, attention_mask, rotary, self.q_norm if fuse_qnorm else None)
         else:
             out = self.forward_attention(q, k, v, attention_mask)
         return out, k_cache, v_cache
