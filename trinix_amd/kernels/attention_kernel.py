@@ -62,11 +62,17 @@ def kernel_head_dim(head_dim: int) -> Optional[int]:
     return None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def current_stream_ptr(device: torch.device) -> int:
     # the raw handle without building a torch.cuda.Stream object (about 2 us
-    # per call less, which shows at small shapes)
+    # per call less, which shows at small shapes); the public route where
+    # this torch build lacks the raw accessor
+    if _raw_stream is None:
+        return torch.cuda.current_stream(device).cuda_stream
     index = device.index if device.index is not None else torch.cuda.current_device()
-    return torch._C._cuda_getCurrentRawStream(index)
+    return _raw_stream(index)
 
 
 def _kernel_ready(t: torch.Tensor) -> bool:
