@@ -65,7 +65,8 @@ typedef enum trinix_status {
   TRINIX_ERR_BAD_STRIDE = 5,     /* d-stride != 1, misaligned rows, or a 16-bit K/V key-row stride >= 2^22 elements */
   TRINIX_ERR_BAD_ARGUMENT = 6,   /* other invalid argument (dropout, ...)   */
   TRINIX_ERR_NO_DEVICE = 7,      /* no gfx950 device / HIP runtime error    */
-  TRINIX_ERR_LAUNCH = 8          /* hipGetLastError after the launch        */
+  TRINIX_ERR_LAUNCH = 8,         /* hipGetLastError after the launch        */
+  TRINIX_ERR_SCRATCH_TOO_SMALL = 9 /* the call needs more than the static scratch */
 } trinix_status;
 
 typedef enum trinix_dtype {
@@ -155,6 +156,23 @@ int trinix_attn_fwd_splitkv_plan(const trinix_attn_fwd_args* args,
                                  int64_t* workspace_bytes);
 int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* args, void* workspace,
                             int64_t workspace_bytes, void* stream);
+
+/* trinix_attn_fwd_splitkv without a workspace argument and without any
+ * allocation: no counterpart in the reference.  It is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  The partial results go to a
+ * static device array of TRINIX_SPLITKV_SCRATCH_BYTES that the library holds
+ * on every GPU it runs on until the process ends (its address is looked up
+ * once per device).  Same arguments, semantics and output as
+ * trinix_attn_fwd_splitkv; `stream` must belong to the current device.
+ * Returns TRINIX_ERR_SCRATCH_TOO_SMALL when the plan's workspace exceeds the
+ * array (the default plan needs at most about 17 MB), before any launch.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams, or host threads) race and must be serialised by
+ * the caller.  Every partial a call reads is written by the same call, so
+ * nothing needs clearing between calls. */
+#define TRINIX_SPLITKV_SCRATCH_BYTES (32u << 20)
+int trinix_attn_fwd_splitkv_noalloc(const trinix_attn_fwd_args* args, void* stream);
 
 /* Block classification of an additive mask of logical size
  * (mb, mh, seqlen_q, seqlen_k) with element strides `stride` (0 = broadcast).

@@ -63,7 +63,7 @@ def test_struct_layout_matches_c(lib, cname, pyty):
 
 def test_version_status_and_tiles(lib):
     assert lib.trinix_abi_version() == nat.ABI_VERSION
-    for code in range(9):
+    for code in range(10):
         assert lib.trinix_status_string(code)
     cfg = nat.TileCfg()
     assert lib.trinix_attn_tile_config(128, nat.TRINIX_BF16, ctypes.byref(cfg)) == 0
@@ -188,6 +188,42 @@ def test_splitkv_rejects_before_launch(lib):
     assert lib.trinix_attn_fwd_splitkv_plan(ctypes.byref(a), None, ctypes.byref(wb)) == nat.TRINIX_ERR_NULL_POINTER
 
 
+def test_splitkv_noalloc_rejects_before_launch(lib, monkeypatch):
+    """The no-allocation entry point validates like trinix_attn_fwd_splitkv
+    and refuses a plan whose workspace exceeds its static scratch, before
+    touching the device (host-only paths)."""
+    dec = dict(seqlen_q=1, seqlen_k=8192, nheads_q=32, nheads_kv=8)
+    assert lib.trinix_attn_fwd_splitkv_noalloc(None, None) == nat.TRINIX_ERR_NULL_POINTER
+    assert lib.trinix_attn_fwd_splitkv_noalloc(ctypes.byref(_args(**dec, head_dim=96)), None) == \
+        nat.TRINIX_ERR_BAD_HEAD_DIM
+    assert lib.trinix_attn_fwd_splitkv_noalloc(ctypes.byref(_args(**dec, dtype=nat.TRINIX_F32)), None) == \
+        nat.TRINIX_ERR_BAD_ARGUMENT
+    assert lib.trinix_attn_fwd_splitkv_noalloc(ctypes.byref(_args(**dict(dec, seqlen_q=17))), None) == \
+        nat.TRINIX_ERR_BAD_ARGUMENT
+    # a tuning override that asks for far more chunks than the default plan
+    big = dict(batch=64, seqlen_q=16, seqlen_k=4096, nheads_q=32, nheads_kv=8)
+    monkeypatch.setenv("TRINIX_SPLITKV_CFG", "65536,64")
+    ns, need = _plan(lib, **big)
+    assert need > nat.SPLITKV_SCRATCH_BYTES
+    assert lib.trinix_attn_fwd_splitkv_noalloc(ctypes.byref(_args(**big)), None) == \
+        nat.TRINIX_ERR_SCRATCH_TOO_SMALL
+    with pytest.raises(ValueError, match="static buffer"):
+        nat.check(nat.TRINIX_ERR_SCRATCH_TOO_SMALL, "trinix_attn_fwd_splitkv_noalloc")
+
+
+def test_splitkv_default_plan_fits_static_scratch(lib):
+    """The default plan never asks for more than the no-allocation entry
+    point's scratch: the largest workspace comes from just under 1024
+    (batch, KV head, 16-row) items, split in two, 16 rows each at D=128."""
+    worst = 0
+    for batch in (1, 2, 63, 64, 127, 128, 255, 511, 1023):
+        for sq, hq, hkv in ((16, 8, 8), (16, 32, 8), (1, 32, 8), (4, 32, 8), (16, 4, 1)):
+            for sk in (1 << 10, 1 << 14, 1 << 20):
+                worst = max(worst, _plan(lib, batch=batch, seqlen_q=sq, seqlen_k=sk, nheads_q=hq, nheads_kv=hkv,
+                                         head_dim=128)[1])
+    assert 0 < worst <= 1023 * 16 * 2 * 129 * 4 < nat.SPLITKV_SCRATCH_BYTES
+
+
 def test_qk_norm_rejects_before_launch(lib):
     st = (ctypes.c_int64 * 4)(8 * 64 * 128, 8 * 128, 128, 1)
 
@@ -242,3 +278,4 @@ def test_splitkv_plan_invariants_random(lib):
         assert ns == 1 or (ns - 1) * ((chunk + 63) // 64 * 64) < span
         assert items * ns < 2 ** 31
         assert wb == (0 if ns == 1 else kw["batch"] * Hkv * rows * ns * (kw["head_dim"] + 1) * 4)
+        assert wb <= nat.SPLITKV_SCRATCH_BYTES

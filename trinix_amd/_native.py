@@ -25,6 +25,9 @@ TRINIX_ERR_BAD_STRIDE = 5
 TRINIX_ERR_BAD_ARGUMENT = 6
 TRINIX_ERR_NO_DEVICE = 7
 TRINIX_ERR_LAUNCH = 8
+TRINIX_ERR_SCRATCH_TOO_SMALL = 9
+
+SPLITKV_SCRATCH_BYTES = 32 << 20
 
 TRINIX_F32 = 0
 TRINIX_F16 = 1
@@ -153,6 +156,7 @@ SIGNATURES = {
     ),
     "trinix_attn_fwd_splitkv_plan": (c_int32, [POINTER(AttnFwdArgs), POINTER(c_int32), POINTER(c_int64)]),
     "trinix_attn_fwd_splitkv": (c_int32, [POINTER(AttnFwdArgs), c_void_p, c_int64, c_void_p]),
+    "trinix_attn_fwd_splitkv_noalloc": (c_int32, [POINTER(AttnFwdArgs), c_void_p]),
     "trinix_attn_bwd": (c_int32, [POINTER(AttnBwdArgs), c_void_p]),
     "trinix_qk_norm": (
         c_int32,

@@ -24,6 +24,7 @@
 // The 4 wavefronts' (max, sum, O) are merged through LDS at the end.
 #include <cstdio>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "attn_params.h"
@@ -454,15 +455,11 @@ extern "C" int trinix_attn_fwd_splitkv_plan(const trinix_attn_fwd_args* a, int32
   return TRINIX_OK;
 }
 
-extern "C" int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* a, void* workspace, int64_t workspace_bytes,
-                                       void* stream) {
-  const int rc = validate_fwd_args(a);
-  if (rc != TRINIX_OK) return rc;
-  SplitPlan pl;
-  if (!make_split_plan(a, &pl)) return TRINIX_ERR_BAD_ARGUMENT;
-  if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes || ((uintptr_t)workspace & 15) != 0))
-    return TRINIX_ERR_BAD_ARGUMENT;
+namespace {
 
+// Launches the split-KV forward of a validated call with plan `pl`; the
+// partial results go to `workspace` (pl.ws_bytes bytes, 16-byte aligned).
+int launch_splitkv(const trinix_attn_fwd_args* a, const SplitPlan& pl, void* workspace, hipStream_t st) {
   DecParams p;
   p.q = (const uint16_t*)a->q;
   p.k = (const uint16_t*)a->k;
@@ -502,7 +499,6 @@ extern "C" int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* a, void* work
   p.part_lse = pl.ws_bytes > 0 ? (float*)workspace + nrows * a->head_dim : nullptr;
   const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0);
 
-  hipStream_t st = (hipStream_t)stream;
   (void)hipGetLastError();
   hipError_t err;
   if (a->dtype == TRINIX_BF16)
@@ -510,4 +506,55 @@ extern "C" int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* a, void* work
   else
     err = a->head_dim == 128 ? launch_decode<F16, 128>(p, feat, st) : launch_decode<F16, 64>(p, feat, st);
   return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+}
+
+// Scratch of trinix_attn_fwd_splitkv_noalloc: the partial (O, lse) of every
+// (row, chunk), in device memory that the code object holds on each GPU the
+// library runs on, until the process ends.  In host code the name `scratch`
+// only stands in for the symbol: its address on the current device comes
+// from hipGetSymbolAddress, looked up once per device and kept.
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) float scratch[TRINIX_SPLITKV_SCRATCH_BYTES / sizeof(float)];
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TRINIX_ERR_NO_DEVICE;
+  std::lock_guard<std::mutex> guard(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return TRINIX_ERR_NO_DEVICE;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TRINIX_OK;
+}
+
+}  // namespace
+
+extern "C" int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* a, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  const int rc = validate_fwd_args(a);
+  if (rc != TRINIX_OK) return rc;
+  SplitPlan pl;
+  if (!make_split_plan(a, &pl)) return TRINIX_ERR_BAD_ARGUMENT;
+  if (pl.ws_bytes > 0 && (!workspace || workspace_bytes < pl.ws_bytes || ((uintptr_t)workspace & 15) != 0))
+    return TRINIX_ERR_BAD_ARGUMENT;
+  return launch_splitkv(a, pl, workspace, (hipStream_t)stream);
+}
+
+extern "C" int trinix_attn_fwd_splitkv_noalloc(const trinix_attn_fwd_args* a, void* stream) {
+  const int rc = validate_fwd_args(a);
+  if (rc != TRINIX_OK) return rc;
+  SplitPlan pl;
+  if (!make_split_plan(a, &pl)) return TRINIX_ERR_BAD_ARGUMENT;
+  if (pl.ws_bytes > (int64_t)TRINIX_SPLITKV_SCRATCH_BYTES) return TRINIX_ERR_SCRATCH_TOO_SMALL;
+  void* ws = nullptr;
+  if (pl.ws_bytes > 0) {
+    const int src = scratch_on_current_device(&ws);
+    if (src != TRINIX_OK) return src;
+  }
+  return launch_splitkv(a, pl, ws, (hipStream_t)stream);
 }

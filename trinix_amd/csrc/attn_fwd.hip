@@ -355,6 +355,7 @@ const char* trinix_status_string(int status) {
     case TRINIX_ERR_BAD_ARGUMENT: return "invalid argument";
     case TRINIX_ERR_NO_DEVICE: return "no gfx950 device available";
     case TRINIX_ERR_LAUNCH: return "kernel launch failed";
+    case TRINIX_ERR_SCRATCH_TOO_SMALL: return "the call needs more scratch than the library's static buffer holds (TRINIX_SPLITKV_SCRATCH_BYTES); use the entry point that takes a workspace";
     default: return "unknown status";
   }
 }
