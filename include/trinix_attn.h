@@ -54,13 +54,13 @@
 extern "C" {
 #endif
 
-#define TRINIX_ATTN_ABI_VERSION 2
+#define TRINIX_ATTN_ABI_VERSION 3
 
 typedef enum trinix_status {
   TRINIX_OK = 0,
   TRINIX_ERR_NULL_POINTER = 1,   /* a required pointer is NULL             */
   TRINIX_ERR_BAD_DTYPE = 2,      /* unsupported dtype / dtype mismatch      */
-  TRINIX_ERR_BAD_HEAD_DIM = 3,   /* head_dim not built for the entry point (forward: 64, 128, 256; backward, split-KV: 64, 128) */
+  TRINIX_ERR_BAD_HEAD_DIM = 3,   /* head_dim not built for the entry point (forward, backward: 64, 128, 256; split-KV: 64, 128) */
   TRINIX_ERR_BAD_SHAPE = 4,      /* non-positive or inconsistent sizes      */
   TRINIX_ERR_BAD_STRIDE = 5,     /* d-stride != 1, misaligned rows, or a 16-bit K/V key-row stride >= 2^22 elements */
   TRINIX_ERR_BAD_ARGUMENT = 6,   /* other invalid argument (dropout, ...)   */
@@ -223,17 +223,22 @@ int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* out,
                    const void* sin, int64_t cs_stride, int64_t cs_rows,
                    const int64_t* position_ids, void* stream);
 
-/* Backward of trinix_attn_fwd for bf16/fp16 without dropout.  No
- * counterpart in the reference (its Triton attention has no backward,
- * attention_kernel.py:497-517); the gradients are those of the eager path
- * softmax(scale*q k^T + ALiBi + mask) v (base.py:347-400):
- *   dv = P^T dout, dz = P*(dout v^T - rowsum(dout*out)), dq = scale*dz k,
- *   dk = scale*dz^T q (summed over the q-heads sharing a KV head).
+/* Backward of trinix_attn_fwd.  No counterpart in the reference (its
+ * Triton attention has no backward, attention_kernel.py:497-517); the
+ * gradients are those of the eager path
+ * dropout(softmax(scale*q k^T + ALiBi + mask)) v (base.py:347-400):
+ *   P  = softmax(z),  Pd = P * keep / (1 - dropout_p)
+ *   dv = Pd^T dout,  dz = P*(keep*(dout v^T)/(1 - dropout_p) - rowsum(dout*out)),
+ *   dq = scale*dz k,  dk = scale*dz^T q (summed over the q-heads sharing a KV head).
+ * keep is the forward's dropout mask, regenerated from the same
+ * dropout_seed / dropout_offset (pass those of the forward call).
+ * dtype fp32, bf16 or fp16; head_dim 64, 128 or 256.
  * q, k, v, out, dout and the outputs dq (like q), dk, dv (like k, v) are
  * BSHD with d stride 1; lse is the (B, Hq, Sq) fp32 natural-log row
  * log-sum-exp written by trinix_attn_fwd; delta is a caller-provided fp32
  * workspace of B*Hq*Sq elements.  Scale, causal, window, ALiBi and mask
- * arguments mean what they mean in trinix_attn_fwd_args. */
+ * arguments mean what they mean in trinix_attn_fwd_args.  ABI version 3
+ * appended the three dropout fields. */
 typedef struct trinix_attn_bwd_args {
   const void* q;
   const void* k;
@@ -266,6 +271,9 @@ typedef struct trinix_attn_bwd_args {
   int64_t mask_stride[4];
   const uint8_t* mask_blockmap;
   int64_t blockmap_stride[2];
+  float dropout_p;              /* the forward's dropout_p, seed and offset */
+  uint64_t dropout_seed;
+  uint64_t dropout_offset;
 } trinix_attn_bwd_args;
 int trinix_attn_bwd(const trinix_attn_bwd_args* args, void* stream);
 

@@ -73,10 +73,13 @@ __all__ = [
 # --------------------------------------------------------------------------
 def eager_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     attn_mask: Optional[torch.Tensor] = None, scale: Optional[float] = None,
-                    causal: bool = False) -> torch.Tensor:
-    """``_apply_pytorch_attention`` with dropout off.  q (B,Sq,H,D), k/v
-    (B,Sk,H,D) with H equal (tile KV first); mask broadcastable to
-    (B,H,Sq,Sk).  Returns (B,Sq,H,D) in q.dtype."""
+                    causal: bool = False, keep: Optional[torch.Tensor] = None,
+                    dropout_p: float = 0.0) -> torch.Tensor:
+    """``_apply_pytorch_attention``.  q (B,Sq,H,D), k/v (B,Sk,H,D) with H
+    equal (tile KV first); mask broadcastable to (B,H,Sq,Sk).  Dropout
+    (base.py:395, ``F.dropout`` after the softmax) uses the given keep mask
+    (B,H,Sq,Sk) instead of a random draw: w * keep / (1 - dropout_p).
+    Returns (B,Sq,H,D) in q.dtype."""
     B, S, H, D = q.shape
     Sk = k.shape[1]
     if scale is None:
@@ -97,6 +100,8 @@ def eager_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         m = m.expand(B, H, S, Sk).reshape(B * H, S, Sk)
         w += m
     w = F.softmax(w, dim=-1)
+    if keep is not None:
+        w = w * keep.reshape(B * H, S, Sk).to(w.dtype) * (1.0 / (1.0 - dropout_p))
     out = torch.bmm(w, vh)
     return out.reshape(B, H, S, D).transpose(1, 2)
 
@@ -186,7 +191,8 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                          causal: bool = False, window_size: Optional[Tuple[int, int]] = None,
                          alibi_slopes: Optional[torch.Tensor] = None,
                          heads: Optional[Sequence[int]] = None, batches: Optional[Sequence[int]] = None,
-                         head_chunk: int = 1) -> torch.Tensor:
+                         head_chunk: int = 1, keep: Optional[torch.Tensor] = None,
+                         dropout_p: float = 0.0) -> torch.Tensor:
     """What ``triton_attn_func`` computes, on the CPU through ``eager_attention``.
 
     GQA/MQA KV is tiled (grouped_query_attention.py:140-145).  Window, user
@@ -195,6 +201,8 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ``heads`` / ``batches`` restrict the evaluation to a subset (heads are
     independent); results are (len(batches), Sq, len(heads), D).  The work is
     chunked over (b, head_chunk heads) to bound the S^2 score memory.
+    ``keep`` (B,H,Sq,Sk) bool with ``dropout_p``: dropout with that mask
+    (``dropout_keep`` gives the kernel's).
     """
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
@@ -235,7 +243,8 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 sb = slopes[b if slopes.shape[0] > 1 else 0]
                 ab = alibi_bias(Sq, Sk, sb[hs])[None]
                 m = ab if m is None else m + ab
-            row.append(eager_attention(qs, ks, vs, m, softmax_scale, causal))
+            kp = None if keep is None else keep[b:b + 1, hs]
+            row.append(eager_attention(qs, ks, vs, m, softmax_scale, causal, kp, dropout_p))
         outs.append(torch.cat(row, dim=2))
     return torch.cat(outs, dim=0)
 
@@ -267,9 +276,11 @@ def _bias64(Sq, Sk, H, B, attn_mask, causal, window_size, alibi_slopes):
 
 
 def closed_form(q, k, v, attn_mask=None, softmax_scale=None, causal=False, window_size=None,
-                alibi_slopes=None) -> np.ndarray:
+                alibi_slopes=None, keep=None, dropout_p=0.0) -> np.ndarray:
     """float64 ``softmax(q k^T * scale + bias) v`` from the same (rounded)
-    inputs; GQA by ``h // (H/Hkv)``.  Returns (B,Sq,H,D) float64."""
+    inputs; GQA by ``h // (H/Hkv)``; with ``keep`` (B,H,Sq,Sk) the
+    probabilities are multiplied by keep / (1 - dropout_p).  Returns
+    (B,Sq,H,D) float64."""
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     if softmax_scale is None:
@@ -283,6 +294,8 @@ def closed_form(q, k, v, attn_mask=None, softmax_scale=None, causal=False, windo
         mx = s.max(axis=-1, keepdims=True)
         p = np.exp(s - mx)
         p = p / p.sum(axis=-1, keepdims=True)
+    if keep is not None:
+        p = p * np.asarray(keep, dtype=np.float64) / (1.0 - dropout_p)
     return np.einsum("bhij,bjhd->bihd", p, vd)
 
 

@@ -5,15 +5,14 @@ The reference pads head_dim to the next power of two
 D = 256 models run on its Triton path.  Here the forward kernels are built
 for D = 256 (one wavefront per SIMD, 128 KiB of LDS per workgroup); D in
 (128, 256) is zero-padded to 256.  Same oracle and bar as the other parity
-tests.  The backward is built for D <= 128: with gradients required, D = 256
-keeps the reference's detached output and warns.
+tests.  D = 256 is differentiable through the generic backward kernels
+(gradients tested in test_attn_bwd_gpu.py).
 """
 import pytest
 import torch
 
 from oracle import attention_oracle as orc
 from trinix_amd import triton_attn_func
-from trinix_amd.kernels import attention_kernel as ak
 from test_attn_gpu import assert_parity, assert_parity_or_more_accurate, oracle_on, rand
 
 pytestmark = pytest.mark.gpu
@@ -64,10 +63,9 @@ def test_head_dim_256_alibi_mask_rope_lse(dtype):
     assert torch.allclose(lse.cpu().double(), torch.logsumexp(s, dim=-1), atol=2e-3, rtol=1e-4)
 
 
-def test_head_dim_256_with_grad_warns_and_detaches():
-    ak._warned_no_grad.clear()
+def test_head_dim_256_with_grad_is_differentiable():
     q, k, v = (rand((1, 64, 2, 256), torch.bfloat16, 221 + i).requires_grad_(True) for i in range(3))
-    with pytest.warns(UserWarning, match="detached"):
-        out = triton_attn_func(q, k, v, causal=True)
-    assert out.grad_fn is None
-    assert_parity(out, oracle_on(q.detach(), k.detach(), v.detach(), causal=True), torch.bfloat16, "d256 grad")
+    out = triton_attn_func(q, k, v, causal=True)
+    assert out.grad_fn is not None
+    assert_parity(out.detach(), oracle_on(q.detach(), k.detach(), v.detach(), causal=True), torch.bfloat16,
+                  "d256 grad")

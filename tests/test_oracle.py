@@ -193,6 +193,32 @@ def test_dropout_keep_statistics():
     assert np.array_equal(keep, orc.dropout_keep(2, 3, 64, 100, 0.25, seed=77))
 
 
+def test_dropout_in_eager_restatement_pinned():
+    """Dropout with a given keep mask (base.py:395): against the fp64
+    closed form, and two cases the mathematics fixes: a mask keeping
+    everything scales the no-dropout output by 1/(1-p), a mask keeping
+    nothing gives zeros; a row keeping one key c gives P[c] v[c] / (1-p)."""
+    g = torch.Generator().manual_seed(9)
+    B, S, H, D, p = 2, 12, 3, 8, 0.4
+    q, k, v = (torch.randn(B, S, H, D, generator=g) for _ in range(3))
+    keep = torch.from_numpy(orc.dropout_keep(B, H, S, S, p, seed=5))
+    out = orc.functional_attention(q, k, v, causal=True, keep=keep, dropout_p=p)
+    ref = orc.closed_form(q, k, v, causal=True, keep=keep.numpy(), dropout_p=p)
+    assert np.allclose(out.double().numpy(), ref, rtol=1e-5, atol=1e-6)
+    plain = orc.functional_attention(q, k, v, causal=True)
+    ones = torch.ones(B, H, S, S, dtype=torch.bool)
+    got = orc.functional_attention(q, k, v, causal=True, keep=ones, dropout_p=p)
+    assert torch.allclose(got, plain / (1 - p), rtol=1e-6, atol=1e-6)
+    assert torch.equal(orc.functional_attention(q, k, v, keep=~ones, dropout_p=p), torch.zeros(B, S, H, D))
+    one = torch.zeros(B, H, S, S, dtype=torch.bool)
+    one[..., 3] = True
+    got = orc.functional_attention(q, k, v, keep=one, dropout_p=p)
+    s = torch.einsum("bihd,bjhd->bhij", q.double(), k.double()) * D ** -0.5
+    pc = torch.softmax(s, -1)[..., 3]  # (B, H, Sq)
+    want = pc.permute(0, 2, 1)[..., None] * v.double()[:, 3][:, None] / (1 - p)
+    assert torch.allclose(got.double(), want, rtol=1e-5, atol=1e-6)
+
+
 def test_allowed_pairs_and_flops():
     for Sq, Sk, causal, win in [(7, 7, True, None), (9, 5, True, None), (10, 10, False, (2, 1)),
                                 (12, 12, True, (3, 0)), (6, 9, False, None), (8, 8, True, (0, 0))]:

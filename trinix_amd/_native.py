@@ -37,7 +37,7 @@ TRINIX_U8 = 3
 BLOCKMAP_ROWS = 32
 BLOCKMAP_COLS = 64
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 Int64x4 = c_int64 * 4
 Int64x2 = c_int64 * 2
@@ -127,6 +127,9 @@ class AttnBwdArgs(ctypes.Structure):
         ("mask_stride", Int64x4),
         ("mask_blockmap", c_void_p),
         ("blockmap_stride", Int64x2),
+        ("dropout_p", c_float),
+        ("dropout_seed", c_uint64),
+        ("dropout_offset", c_uint64),
     ]
 
 

@@ -1,8 +1,11 @@
 // Host entry point of the attention backward (C ABI) and the delta pre-pass.
 //
 // trinix_attn_bwd validates the arguments, computes delta = rowsum(dO * O)
-// into the caller's workspace and launches the dK/dV and dQ kernels
-// (attn_bwd16.h, instantiated per (dtype, head_dim) in attn_bwd16_*.hip).
+// into the caller's workspace and launches the dK/dV and dQ kernels: the
+// bf16/fp16 MFMA pipeline (attn_bwd16.h, instantiated per (dtype, head_dim)
+// in attn_bwd16_*.hip) for head_dim 64/128 without dropout, the generic
+// fp32-product kernels (attn_bwd_generic.hip) for fp32, head_dim 256 and
+// dropout.
 #include <cstdint>
 
 #include "attn_bwd16.h"
@@ -46,6 +49,13 @@ void launch_delta(const BwdParams& p, hipStream_t st) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
+// fp32 BSHD tensor (generic kernels, element loads): head_dim stride 1.
+int check32(const void* ptr, const int64_t st[4]) {
+  if (!ptr) return TRINIX_ERR_NULL_POINTER;
+  if (st[3] != 1 || ((uintptr_t)ptr & 3) != 0) return TRINIX_ERR_BAD_STRIDE;
+  return TRINIX_OK;
+}
+
 // 16-bit BSHD tensor: head_dim stride 1, 16-byte aligned rows, and a row
 // stride the 32-bit in-tile offsets can address (tiles of up to 128 rows).
 int check16(const void* ptr, const int64_t st[4]) {
@@ -64,8 +74,9 @@ using namespace trinix;
 
 extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   if (!a) return TRINIX_ERR_NULL_POINTER;
-  if (a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F32) return TRINIX_ERR_BAD_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
   if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0 ||
       a->nheads_q % a->nheads_kv != 0)
     return TRINIX_ERR_BAD_SHAPE;
@@ -73,10 +84,10 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
     return TRINIX_ERR_BAD_SHAPE;
   if (!a->lse || !a->delta) return TRINIX_ERR_NULL_POINTER;
   int rc;
-  if ((rc = check16(a->q, a->q_stride)) || (rc = check16(a->k, a->k_stride)) || (rc = check16(a->v, a->v_stride)) ||
-      (rc = check16(a->out, a->out_stride)) || (rc = check16(a->dout, a->dout_stride)) ||
-      (rc = check16(a->dq, a->dq_stride)) || (rc = check16(a->dk, a->dk_stride)) ||
-      (rc = check16(a->dv, a->dv_stride)))
+  auto check = a->dtype == TRINIX_F32 ? check32 : check16;
+  if ((rc = check(a->q, a->q_stride)) || (rc = check(a->k, a->k_stride)) || (rc = check(a->v, a->v_stride)) ||
+      (rc = check(a->out, a->out_stride)) || (rc = check(a->dout, a->dout_stride)) ||
+      (rc = check(a->dq, a->dq_stride)) || (rc = check(a->dk, a->dk_stride)) || (rc = check(a->dv, a->dv_stride)))
     return rc;
   if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
       a->mask_dtype != TRINIX_U8)
@@ -128,11 +139,26 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.num_mblk = (int)((a->seqlen_q + 127) / 128);
   if ((int64_t)p.B * p.Hq * p.num_mblk >= (1ll << 31) || (int64_t)p.B * p.Hkv * p.num_kblk >= (1ll << 31))
     return TRINIX_ERR_BAD_SHAPE;
+  p.use_dropout = a->dropout_p > 0.f ? 1 : 0;
+  {
+    const double th = (double)a->dropout_p * 4294967296.0;
+    p.drop_thresh = th >= 4294967295.0 ? 0xffffffffu : (uint32_t)th;
+    p.drop_scale = a->dropout_p > 0.f ? 1.f / (1.f - a->dropout_p) : 1.f;
+  }
+  p.seed_lo = (uint32_t)a->dropout_seed;
+  p.seed_hi = (uint32_t)(a->dropout_seed >> 32);
+  p.off_lo = (uint32_t)a->dropout_offset;
+  p.off_hi = (uint32_t)(a->dropout_offset >> 32);
   const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0);
 
   hipStream_t st = (hipStream_t)stream;
   (void)hipGetLastError();
   hipError_t err;
+  if (a->dtype == TRINIX_F32 || a->head_dim == 256 || p.use_dropout) {
+    err = launch_bwd_generic(p, a->dtype, (int)a->head_dim, st);
+    if (err == hipErrorInvalidValue) return TRINIX_ERR_BAD_SHAPE;
+    return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+  }
   const bool bf = a->dtype == TRINIX_BF16;
   if (a->head_dim == 128) {
     if (bf) launch_delta<BF16, 128>(p, st);

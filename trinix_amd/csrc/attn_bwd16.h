@@ -55,6 +55,11 @@ struct BwdParams {
   int64_t bm_sb, bm_sh;
   int bm_cols;
   int num_kblk, num_mblk;  // 128-key blocks (dK/dV), 128-row blocks (dQ)
+  // dropout of the forward (attn_params.h dropout_group): same Philox stream
+  int use_dropout;
+  uint32_t drop_thresh;  // dropped when the Philox word < drop_thresh
+  float drop_scale;      // 1 / (1 - p)
+  uint32_t seed_lo, seed_hi, off_lo, off_hi;
 };
 
 // Allowed (i, j): j - i in [dlo, dhi] (causal: j <= i; window: -wl <= j-i <= wr).
@@ -719,5 +724,10 @@ hipError_t launch_bwd16_bf16_d64(const BwdParams& p, int feat, hipStream_t st);
 hipError_t launch_bwd16_bf16_d128(const BwdParams& p, int feat, hipStream_t st);
 hipError_t launch_bwd16_f16_d64(const BwdParams& p, int feat, hipStream_t st);
 hipError_t launch_bwd16_f16_d128(const BwdParams& p, int feat, hipStream_t st);
+
+// The generic backward (attn_bwd_generic.hip): fp32 products, any dtype
+// (TRINIX_F32 / F16 / BF16), head_dim 64, 128 or 256, dropout, ALiBi and
+// mask read per element.  Launches its own delta pre-pass.
+hipError_t launch_bwd_generic(const BwdParams& p, int dtype, int D, hipStream_t st);
 
 }  // namespace trinix

@@ -349,7 +349,7 @@ const char* trinix_status_string(int status) {
     case TRINIX_OK: return "ok";
     case TRINIX_ERR_NULL_POINTER: return "a required pointer is NULL";
     case TRINIX_ERR_BAD_DTYPE: return "unsupported dtype";
-    case TRINIX_ERR_BAD_HEAD_DIM: return "unsupported head_dim (forward kernels are built for 64, 128 and 256; backward for 64 and 128)";
+    case TRINIX_ERR_BAD_HEAD_DIM: return "unsupported head_dim (forward and backward kernels are built for 64, 128 and 256; split-KV for 64 and 128)";
     case TRINIX_ERR_BAD_SHAPE: return "invalid or inconsistent sizes";
     case TRINIX_ERR_BAD_STRIDE: return "unsupported strides or alignment (head_dim stride must be 1, 16-byte aligned rows, 16-bit K/V key-row stride below 2^22 elements)";
     case TRINIX_ERR_BAD_ARGUMENT: return "invalid argument";

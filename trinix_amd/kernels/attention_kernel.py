@@ -24,7 +24,6 @@ from __future__ import annotations
 
 import ctypes
 import math
-import warnings
 from typing import Optional, Tuple
 
 import torch
@@ -43,8 +42,9 @@ _MASK_DTYPE_CODE = {
     torch.uint8: nat.TRINIX_U8,
 }
 KERNEL_HEAD_DIMS = (64, 128, 256)
-# The backward kernels are built for these (the forward for all of the above).
-BACKWARD_HEAD_DIMS = (64, 128)
+# The backward kernels are built for the same widths (bf16/fp16 at 64 and
+# 128 without dropout run the MFMA pipeline, the rest the generic kernels).
+BACKWARD_HEAD_DIMS = (64, 128, 256)
 
 
 # Calls with at most this many query rows (bf16/fp16, no dropout) go to the
@@ -330,6 +330,11 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             args.blockmap_stride = nat.int64x2(bst)
 
     if dropout_p > 0.0:
+        if torch.cuda.is_current_stream_capturing():
+            # the seed becomes a kernel argument: every replay would drop
+            # the same elements
+            raise RuntimeError("attention dropout cannot be captured in a HIP graph (the seed would be frozen); "
+                               "capture with dropout_p=0")
         # Seed from torch's CPU generator: no device->host sync.
         args.dropout_p = float(dropout_p)
         args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
@@ -371,7 +376,8 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
     state = None
     if keep_state:
         state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),
-                     window=window_size, D=D, d_kernel=d_kernel, keep=keep, args=args)
+                     window=window_size, D=D, d_kernel=d_kernel, keep=keep, args=args,
+                     dropout=(float(args.dropout_p), int(args.dropout_seed), int(args.dropout_offset)))
     if d_kernel != D:
         out = out[..., :D].contiguous()
     return out, lse, state
@@ -405,6 +411,7 @@ def _backward(state, dout):
     a.alibi_slopes, a.alibi_stride = fa.alibi_slopes, fa.alibi_stride
     a.mask, a.mask_dtype, a.mask_stride = fa.mask, fa.mask_dtype, fa.mask_stride
     a.mask_blockmap, a.blockmap_stride = fa.mask_blockmap, fa.blockmap_stride
+    a.dropout_p, a.dropout_seed, a.dropout_offset = state["dropout"]
     rc = nat.load_library().trinix_attn_bwd(ctypes.byref(a), current_stream_ptr(qk.device))
     nat.check(rc, "trinix_attn_bwd")
     if dkrn != D:
@@ -419,8 +426,8 @@ class _HipAttnFunction(torch.autograd.Function):
     rotated back (the RoPE kernel with -sin) in the backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, attn_mask, causal, scale, window_size, alibi_slopes, rotary_cos, rotary_sin, rotary_k,
-                return_lse):
+    def forward(ctx, q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, rotary_cos, rotary_sin,
+                rotary_k, return_lse):
         from .rope_kernel import rope_apply
 
         ctx.rope = None
@@ -429,8 +436,8 @@ class _HipAttnFunction(torch.autograd.Function):
             if rotary_k:
                 k = rope_apply(k, rotary_cos, rotary_sin)
             ctx.rope = (rotary_cos, rotary_sin, rotary_k)
-        out, lse, state = _forward(q, k, v, attn_mask, causal, scale, 0.0, window_size, alibi_slopes, None, None,
-                                   True, True, True, keep_state=True)
+        out, lse, state = _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, None,
+                                   None, True, True, True, keep_state=True)
         ctx.state = state
         if return_lse:
             ctx.mark_non_differentiable(lse)
@@ -449,40 +456,38 @@ class _HipAttnFunction(torch.autograd.Function):
             dq = rope_apply(dq, cos, neg)
             if rot_k:
                 dk = rope_apply(dk, cos, neg)
-        return dq, dk, dv, None, None, None, None, None, None, None, None, None
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
 
 
-_warned_no_grad = set()
+def backward_supported(q: torch.Tensor) -> bool:
+    """True if ``trinix_attn_bwd`` covers attention on ``q`` (every dtype the
+    forward takes, dropout included, at a kernel head_dim)."""
+    return q.dtype in _DTYPE_CODE and kernel_head_dim(q.shape[-1]) in BACKWARD_HEAD_DIMS
 
 
 def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, window_size=None, alibi_slopes=None,
               *, rotary_cos=None, rotary_sin=None, rotary_k=True, return_lse=False, q_norm_weight=None,
               q_norm_eps=1e-6):
-    """Attention with gradients when q, k or v require them (bf16/fp16, no
-    dropout, head_dim <= 128); otherwise ``TritonAttentionKernel.apply``.
+    """Attention with gradients when q, k or v require them; otherwise
+    ``TritonAttentionKernel.apply``.
 
     The reference's Triton attention has no backward (its output is detached,
-    ``attention_kernel.py:497-517``).  Here bf16/fp16 attention without
-    dropout and with head_dim <= 128 is differentiable through
-    ``trinix_attn_bwd``.  fp32, dropout or head_dim > 128 with gradients
-    required keep the reference's behaviour, a detached output, and warn once.
+    ``attention_kernel.py:497-517``).  Here it is differentiable through
+    ``trinix_attn_bwd`` for fp32, bf16 and fp16, with dropout (the backward
+    regenerates the forward's keep mask), head_dim up to 256.  A call the
+    backward does not cover while gradients are required raises instead of
+    returning a detached output.
     """
     needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
     if q_norm_weight is not None and (needs_grad or (torch.is_grad_enabled() and q_norm_weight.requires_grad)):
         raise ValueError("the fused q RMSNorm has no backward: apply the norm module before attention() to train")
     if needs_grad:
-        dk = kernel_head_dim(q.shape[-1])
-        if q.dtype in (torch.float16, torch.bfloat16) and dropout_p == 0.0 and dk in BACKWARD_HEAD_DIMS:
-            if scale is None:
-                scale = q.shape[-1] ** -0.5
-            return _HipAttnFunction.apply(q, k, v, attn_mask, causal, scale, window_size, alibi_slopes, rotary_cos,
-                                          rotary_sin, rotary_k, return_lse)
-        key = (q.dtype, dropout_p > 0.0, dk)
-        if key not in _warned_no_grad:
-            _warned_no_grad.add(key)
-            warnings.warn("HIP attention backward runs in bf16/fp16 without dropout, head_dim <= 128; this "
-                          "call's output is detached (no gradient flows through it), as in the reference "
-                          "Triton path", stacklevel=2)
+        if not backward_supported(q):
+            raise ValueError(f"no HIP attention backward for dtype {q.dtype}, head_dim {q.shape[-1]}")
+        if scale is None:
+            scale = q.shape[-1] ** -0.5
+        return _HipAttnFunction.apply(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes,
+                                      rotary_cos, rotary_sin, rotary_k, return_lse)
     return TritonAttentionKernel.apply(q, k, v, attn_mask=attn_mask, causal=causal, scale=scale, dropout_p=dropout_p,
                                        window_size=window_size, alibi_slopes=alibi_slopes, rotary_cos=rotary_cos,
                                        rotary_sin=rotary_sin, rotary_k=rotary_k, return_lse=return_lse,

@@ -45,9 +45,9 @@ def triton_attn_func(
         return_lse: also return the fp32 (B, H, Sq) log-sum-exp.
 
     Returns:
-        (batch, seq_len_q, num_heads, head_dim) tensor of q.dtype.  For
-        bf16/fp16 inputs without dropout it is differentiable (HIP backward;
-        the reference's output is detached).
+        (batch, seq_len_q, num_heads, head_dim) tensor of q.dtype,
+        differentiable through the HIP backward (dropout included; the
+        reference's output is detached).
 
     Raises:
         ValueError: non-GPU tensors or inconsistent shapes.
