@@ -167,17 +167,22 @@ def alibi_slopes(num_heads: int) -> torch.Tensor:
     return torch.tensor(sl, dtype=torch.float32)
 
 
-def alibi_bias(seqlen_q: int, seqlen_k: int, slopes: torch.Tensor) -> torch.Tensor:
-    """(H, Sq, Sk) fp32 bias ``-slope * |i - j|`` (alibi.py:79-90)."""
-    pos = torch.arange(seqlen_k).unsqueeze(0) - torch.arange(seqlen_q).unsqueeze(1)
+def alibi_bias(seqlen_q: int, seqlen_k: int, slopes: torch.Tensor, row0: int = 0, key0: int = 0) -> torch.Tensor:
+    """(H, Sq, Sk) fp32 bias ``-slope * |i - j|`` (alibi.py:79-90) for query
+    positions row0.. and key positions key0..."""
+    pos = (torch.arange(seqlen_k) + key0).unsqueeze(0) - (torch.arange(seqlen_q) + row0).unsqueeze(1)
     pos = pos.abs()
     return -(pos.unsqueeze(0) * slopes.float().view(-1, 1, 1))
 
 
-def window_bias(seqlen_q: int, seqlen_k: int, wl: int, wr: int) -> torch.Tensor:
-    """(Sq, Sk) fp32: 0 where -wl <= j - i <= wr, else -inf."""
-    d = torch.arange(seqlen_k).unsqueeze(0) - torch.arange(seqlen_q).unsqueeze(1)
+def window_bias(seqlen_q: int, seqlen_k: int, wl: int, wr: int, row0: int = 0, key0: int = 0,
+                causal: bool = False) -> torch.Tensor:
+    """(Sq, Sk) fp32: 0 where -wl <= j - i <= wr (and j <= i if causal),
+    else -inf, for query positions row0.. and key positions key0..."""
+    d = (torch.arange(seqlen_k) + key0).unsqueeze(0) - (torch.arange(seqlen_q) + row0).unsqueeze(1)
     ok = (d >= -wl) & (d <= wr)
+    if causal:
+        ok &= d <= 0
     m = torch.zeros(seqlen_q, seqlen_k)
     m[~ok] = float("-inf")
     return m
@@ -192,7 +197,8 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                          alibi_slopes: Optional[torch.Tensor] = None,
                          heads: Optional[Sequence[int]] = None, batches: Optional[Sequence[int]] = None,
                          head_chunk: int = 1, keep: Optional[torch.Tensor] = None,
-                         dropout_p: float = 0.0) -> torch.Tensor:
+                         dropout_p: float = 0.0, rows: Optional[Tuple[int, int]] = None,
+                         keys: Optional[Tuple[int, int]] = None) -> torch.Tensor:
     """What ``triton_attn_func`` computes, on the CPU through ``eager_attention``.
 
     GQA/MQA KV is tiled (grouped_query_attention.py:140-145).  Window, user
@@ -203,6 +209,13 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     chunked over (b, head_chunk heads) to bound the S^2 score memory.
     ``keep`` (B,H,Sq,Sk) bool with ``dropout_p``: dropout with that mask
     (``dropout_keep`` gives the kernel's).
+
+    ``rows`` = (r0, r1) evaluates query rows r0..r1-1 only (a row band: rows
+    are independent), ``keys`` = (k0, k1) restricts the keys to k0..k1-1,
+    which must hold every key the causal / window band lets those rows see
+    (checked).  With either, causal and window masks are folded into the
+    additive mask at the absolute positions (0 / -inf added to the scores,
+    the same values masked_fill gives).
     """
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
@@ -211,9 +224,36 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     heads = list(range(H)) if heads is None else list(heads)
     batches = list(range(B)) if batches is None else list(batches)
     factor = H // Hkv
+    r0, k0 = 0, 0
+    if rows is not None or keys is not None:
+        r0, r1 = rows if rows is not None else (0, Sq)
+        k0, k1 = keys if keys is not None else (0, Sk)
+        lo, hi = -math.inf, math.inf
+        if window_size is not None:
+            lo, hi = -window_size[0], window_size[1]
+        if causal:
+            hi = min(hi, 0)
+        # keys rows r0..r1-1 may see: [max(0, r0 + lo), min(Sk - 1, r1 - 1 + hi)]
+        need_lo = 0 if lo == -math.inf else max(0, r0 + lo)
+        need_hi = Sk - 1 if hi == math.inf else min(Sk - 1, r1 - 1 + hi)
+        assert k0 <= need_lo and k1 - 1 >= need_hi, "key range does not cover the rows' band"
+        q = q[:, r0:r1]
+        k = k[:, k0:k1]
+        v = v[:, k0:k1]
+        if attn_mask is not None and attn_mask.shape[-2] != 1:
+            attn_mask = attn_mask[..., r0:r1, :]
+        if attn_mask is not None and attn_mask.shape[-1] != 1:
+            attn_mask = attn_mask[..., k0:k1]
+        if keep is not None:
+            keep = keep[:, :, r0:r1, k0:k1]
+        wl, wr = (window_size if window_size is not None else (Sk + Sq, Sk + Sq))
+        Sq, Sk = r1 - r0, k1 - k0
+        window_size = (int(wl), int(wr))
     base = None
     if window_size is not None:
-        base = window_bias(Sq, Sk, int(window_size[0]), int(window_size[1]))
+        base = window_bias(Sq, Sk, int(window_size[0]), int(window_size[1]), r0, k0,
+                           causal=causal and (r0, k0) != (0, 0))
+    causal_in_eager = causal and (r0, k0) == (0, 0)
     user = None
     if attn_mask is not None:
         user = attn_mask.float()
@@ -241,10 +281,10 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 m = ub if m is None else m + ub
             if slopes is not None:
                 sb = slopes[b if slopes.shape[0] > 1 else 0]
-                ab = alibi_bias(Sq, Sk, sb[hs])[None]
+                ab = alibi_bias(Sq, Sk, sb[hs], r0, k0)[None]
                 m = ab if m is None else m + ab
             kp = None if keep is None else keep[b:b + 1, hs]
-            row.append(eager_attention(qs, ks, vs, m, softmax_scale, causal, kp, dropout_p))
+            row.append(eager_attention(qs, ks, vs, m, softmax_scale, causal_in_eager, kp, dropout_p))
         outs.append(torch.cat(row, dim=2))
     return torch.cat(outs, dim=0)
 
@@ -252,9 +292,9 @@ def functional_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 # --------------------------------------------------------------------------
 # fp64 closed form and brute force (pins for the restatement above)
 # --------------------------------------------------------------------------
-def _bias64(Sq, Sk, H, B, attn_mask, causal, window_size, alibi_slopes):
+def _bias64(Sq, Sk, H, B, attn_mask, causal, window_size, alibi_slopes, row_pos=None):
     bias = np.zeros((B, H, Sq, Sk), dtype=np.float64)
-    i = np.arange(Sq)[:, None]
+    i = (np.arange(Sq) if row_pos is None else np.asarray(row_pos))[:, None]
     j = np.arange(Sk)[None, :]
     allowed = np.ones((Sq, Sk), dtype=bool)
     if causal:
@@ -270,17 +310,20 @@ def _bias64(Sq, Sk, H, B, attn_mask, causal, window_size, alibi_slopes):
             m = m[None, None]
         elif m.dim() == 3:
             m = m[:, None]
+        if row_pos is not None and m.shape[-2] != 1:
+            m = m[..., list(row_pos), :]
         bias = bias + np.broadcast_to(m.numpy(), (B, H, Sq, Sk))
     bias = np.where(allowed[None, None], bias, -np.inf)
     return bias
 
 
 def closed_form(q, k, v, attn_mask=None, softmax_scale=None, causal=False, window_size=None,
-                alibi_slopes=None, keep=None, dropout_p=0.0) -> np.ndarray:
+                alibi_slopes=None, keep=None, dropout_p=0.0, row_pos=None) -> np.ndarray:
     """float64 ``softmax(q k^T * scale + bias) v`` from the same (rounded)
     inputs; GQA by ``h // (H/Hkv)``; with ``keep`` (B,H,Sq,Sk) the
-    probabilities are multiplied by keep / (1 - dropout_p).  Returns
-    (B,Sq,H,D) float64."""
+    probabilities are multiplied by keep / (1 - dropout_p).  ``row_pos``
+    gives the absolute positions of q's rows (q holds only those rows; the
+    mask is indexed by them).  Returns (B,Sq,H,D) float64."""
     B, Sq, H, D = q.shape
     Sk, Hkv = k.shape[1], k.shape[2]
     if softmax_scale is None:
@@ -289,7 +332,7 @@ def closed_form(q, k, v, attn_mask=None, softmax_scale=None, causal=False, windo
     kd = np.repeat(k.double().numpy(), H // Hkv, axis=2)
     vd = np.repeat(v.double().numpy(), H // Hkv, axis=2)
     s = np.einsum("bihd,bjhd->bhij", qd, kd) * softmax_scale
-    s = s + _bias64(Sq, Sk, H, B, attn_mask, causal, window_size, alibi_slopes)
+    s = s + _bias64(Sq, Sk, H, B, attn_mask, causal, window_size, alibi_slopes, row_pos)
     with np.errstate(invalid="ignore"):
         mx = s.max(axis=-1, keepdims=True)
         p = np.exp(s - mx)

@@ -4,9 +4,10 @@ inputs.
 
 Tolerances (stated by the north star): bf16/fp16 outputs max abs <= 2e-2
 and mean abs <= 2e-3; fp32 outputs ||out - ref||_inf / ||ref||_inf <= 1e-5.
-Large workloads are checked on a subset of (batch, head) against the oracle
-(heads are independent) plus size-independent properties on the full
-problem (GQA == repeated KV bit for bit, stride-0 MQA == materialised KV).
+The BASELINE workloads are checked at full size on every (batch, head) and
+every query row (C4 in row bands with the keys their window can see), plus
+size-independent properties (GQA == repeated KV bit for bit, stride-0 MQA ==
+materialised KV).
 """
 import math
 
@@ -70,6 +71,48 @@ def oracle_on(q, k, v, **kw):
     return orc.functional_attention(q.cpu(), k.cpu(), v.cpu(), **kw)
 
 
+def assert_parity_full(out, ref, dtype, what, q, k, v, row0=0, **kw):
+    """Parity of a full-size output with the oracle, element by element.
+
+    The mean abs error must meet the bar against the oracle.  An element
+    further than the max-abs bar from the oracle passes only where the
+    oracle's own bf16/fp16 arithmetic is more than half the bar away from
+    the fp64 closed form (evaluated for those rows) and the kernel is within
+    the bar of it: at |out| >= 2 one bf16 ulp is 0.0156, so two independent
+    roundings can differ by more than 2e-2 while both are close to the
+    truth.  ``q, k, v`` and ``kw`` are the oracle's inputs (CPU, all rows);
+    ``out`` / ``ref`` row r is query position ``row0 + r``."""
+    out = out.detach().float().cpu()
+    ref = ref.detach().float().cpu()
+    assert out.shape == ref.shape, (what, out.shape, ref.shape)
+    nan_o, nan_r = torch.isnan(out), torch.isnan(ref)
+    assert torch.equal(nan_o, nan_r), f"{what}: NaN pattern differs"
+    ok = ~nan_r
+    d = (out - ref).abs().masked_fill(~ok, 0.0)
+    mean = d[ok].mean().item()
+    assert mean <= 2e-3, f"{what}: mean abs {mean:.4g} (<=2e-3)"
+    bad = (d > 2e-2).nonzero().tolist()
+    rows = {}
+    for b, i, h, _ in bad:
+        rows.setdefault((b, h), set()).add(i)
+    for (b, h), rs in rows.items():
+        rs = sorted(rs)
+        pos = [row0 + i for i in rs]
+        sub_kw = dict(kw)
+        if sub_kw.get("alibi_slopes") is not None:
+            sub_kw["alibi_slopes"] = sub_kw["alibi_slopes"].reshape(-1, q.shape[2])[:, h:h + 1].reshape(-1)
+        hk = h // (q.shape[2] // k.shape[2])
+        x = torch.from_numpy(orc.closed_form(q[b:b + 1, pos][:, :, h:h + 1], k[b:b + 1, :, hk:hk + 1],
+                                             v[b:b + 1, :, hk:hk + 1], row_pos=pos, **sub_kw))[0, :, 0]
+        for r, i in enumerate(rs):
+            for c in (d[b, i, h] > 2e-2).nonzero().flatten().tolist():
+                o_err = abs(ref[b, i, h, c].item() - x[r, c].item())
+                k_err = abs(out[b, i, h, c].item() - x[r, c].item())
+                assert o_err > 1e-2 and k_err <= 2e-2, \
+                    f"{what}: b{b} i{row0 + i} h{h} d{c}: kernel {out[b, i, h, c].item():.5f} oracle {ref[b, i, h, c].item():.5f} " \
+                    f"fp64 {x[r, c].item():.5f}"
+
+
 # ---------------------------------------------------------------------------
 # BASELINE workloads
 # ---------------------------------------------------------------------------
@@ -95,34 +138,48 @@ def test_c2_bf16_causal_mha():
     assert_parity(out, ref, torch.bfloat16, "c2")
 
 
-def test_c3_gqa_rope_causal_subset():
+def test_c3_gqa_rope_causal_every_head_every_row():
+    """C3 at full size against the oracle on every (batch, head) and every
+    query row (a row or work item the kernel never wrote would hold
+    leftover memory and fail)."""
     w = WORKLOADS["c3"]
     inp = make_inputs(w)
     q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
-    out = triton_attn_func(q, k, v, causal=True, rotary_cos=inp.cos.to(DEV), rotary_sin=inp.sin.to(DEV))
-    assert torch.isfinite(out.float()).all()
+    out = triton_attn_func(q, k, v, causal=True, rotary_cos=inp.cos.to(DEV), rotary_sin=inp.sin.to(DEV)).cpu()
     qr = orc.apply_rope(inp.q, inp.cos, inp.sin)
     kr = orc.apply_rope(inp.k, inp.cos, inp.sin)
-    heads = [0, 3, 13, 31]
-    ref = orc.functional_attention(qr, kr, inp.v, causal=True, heads=heads)
-    assert_parity(out[:, :, heads], ref, torch.bfloat16, "c3 heads %s" % heads)
+    ref = orc.functional_attention(qr, kr, inp.v, causal=True, head_chunk=4)
+    assert_parity_full(out, ref, torch.bfloat16, "c3 all heads, all rows", qr, kr, inp.v, causal=True)
+    for r0 in (0, 4096, 8064):  # first, middle and last row block, reported on their own
+        assert_parity_full(out[:, r0:r0 + 128], ref[:, r0:r0 + 128], torch.bfloat16, f"c3 rows {r0}..{r0 + 127}",
+                           qr, kr, inp.v, row0=r0, causal=True)
 
 
-def test_c4_sliding_window_subset():
+def test_c4_sliding_window_every_head_every_row():
+    """C4 at full size against the oracle on every (batch, head) and every
+    query row, in 512-row bands whose key range [r0 - 4096, r0 + 512) holds
+    every key the causal window (4096, 0) lets them see."""
     w = WORKLOADS["c4"]
     inp = make_inputs(w)
     q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
     out = triton_attn_func(q, k, v, causal=True, window_size=w.window, rotary_cos=inp.cos.to(DEV),
-                           rotary_sin=inp.sin.to(DEV))
-    assert torch.isfinite(out.float()).all()
+                           rotary_sin=inp.sin.to(DEV)).cpu()
     qr = orc.apply_rope(inp.q, inp.cos, inp.sin)
     kr = orc.apply_rope(inp.k, inp.cos, inp.sin)
-    ref = orc.functional_attention(qr, kr, inp.v, causal=True, window_size=w.window, heads=[29], batches=[1])
-    assert_parity(out[1:2, :, [29]], ref, torch.bfloat16, "c4 b1 h29")
+    S, wl = w.seqlen, w.window[0]
+    band = 512
+    for r0 in range(0, S, band):
+        keys = (max(0, r0 - wl), r0 + band)
+        ref = orc.functional_attention(qr, kr, inp.v, causal=True, window_size=w.window, rows=(r0, r0 + band),
+                                       keys=keys, head_chunk=8)
+        assert_parity_full(out[:, r0:r0 + band], ref, torch.bfloat16, f"c4 rows {r0}..{r0 + band - 1}",
+                           qr, kr, inp.v, row0=r0, causal=True, window_size=w.window)
 
 
 @pytest.mark.parametrize("name", ["c5a", "c5b"])
-def test_c5_alibi_block_mask_subset(name):
+def test_c5_alibi_block_mask_every_head_every_row(name):
+    """C5a (MHA) / C5b (MQA, stride-0 KV) at full size against the oracle
+    on every (batch, head) and every row."""
     w = WORKLOADS[name]
     inp = make_inputs(w)
     q, k, v = inp.q.to(DEV), inp.k.to(DEV), inp.v.to(DEV)
@@ -131,11 +188,10 @@ def test_c5_alibi_block_mask_subset(name):
         k = k.expand(-1, -1, w.nheads, -1)
         v = v.expand(-1, -1, w.nheads, -1)
         assert k.stride(2) == 0
-    out = triton_attn_func(q, k, v, attn_mask=inp.mask.to(DEV), alibi_slopes=inp.alibi.to(DEV))
-    heads, batches = [0, 9, 15], [0, 7]
-    ref = orc.functional_attention(inp.q, inp.k, inp.v, attn_mask=inp.mask, alibi_slopes=inp.alibi,
-                                   heads=heads, batches=batches)
-    assert_parity(out[batches][:, :, heads], ref, torch.float16, name)
+    out = triton_attn_func(q, k, v, attn_mask=inp.mask.to(DEV), alibi_slopes=inp.alibi.to(DEV)).cpu()
+    ref = orc.functional_attention(inp.q, inp.k, inp.v, attn_mask=inp.mask, alibi_slopes=inp.alibi, head_chunk=8)
+    assert_parity_full(out, ref, torch.float16, name + " all heads, all rows", inp.q, inp.k, inp.v,
+                       attn_mask=inp.mask, alibi_slopes=inp.alibi)
 
 
 def test_gqa_equals_repeated_kv_bitwise():

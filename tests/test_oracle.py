@@ -264,3 +264,43 @@ def test_qk_rms_norm_pinned():
     yb = orc.qk_rms_norm(x.bfloat16(), w.bfloat16(), 1e-6)
     assert yb.dtype == torch.bfloat16
     assert (yb.float() - y).abs().max() <= 2 ** -6 * y.abs().max()
+
+
+def test_row_and_key_bands_equal_full_evaluation():
+    """A row band (and a key range covering the band) gives the rows of the
+    full evaluation: causal, window, ALiBi and a user mask at absolute
+    positions.  Pins the band evaluation the full-size GPU parity tests use."""
+    g = torch.Generator().manual_seed(21)
+    B, S, H, Hkv, D = 2, 96, 4, 2, 16
+    q, k, v = (torch.randn(B, S, h, D, generator=g).bfloat16() for h in (H, Hkv, Hkv))
+    m = torch.randn(S, S, generator=g)
+    sl = orc.alibi_slopes(H)
+    for kw, rows, keys in [
+        (dict(causal=True), (32, 64), None),
+        (dict(causal=True), (0, 16), (0, 16)),
+        (dict(causal=True, window_size=(20, 0)), (40, 72), (20, 72)),
+        (dict(window_size=(5, 9)), (50, 60), (45, 69)),
+        (dict(attn_mask=m, alibi_slopes=sl), (10, 30), None),
+        (dict(causal=True, alibi_slopes=sl, attn_mask=m), (70, 96), (0, 96)),
+    ]:
+        full = orc.functional_attention(q, k, v, **kw)
+        band = orc.functional_attention(q, k, v, rows=rows, keys=keys, **kw)
+        want = full[:, rows[0]:rows[1]]
+        assert band.shape == want.shape
+        assert (band.float() - want.float()).abs().max().item() <= 2 ** -7 * want.float().abs().max().item(), kw
+    with pytest.raises(AssertionError):
+        orc.functional_attention(q, k, v, causal=True, window_size=(20, 0), rows=(40, 72), keys=(30, 72))
+
+
+def test_closed_form_row_positions():
+    """closed_form on a subset of rows with their absolute positions equals
+    those rows of the full evaluation (causal, window, ALiBi, mask)."""
+    g = torch.Generator().manual_seed(23)
+    B, S, H, D = 1, 40, 2, 8
+    q, k, v = (torch.randn(B, S, H, D, generator=g) for _ in range(3))
+    m = torch.randn(S, S, generator=g)
+    for kw in (dict(causal=True), dict(window_size=(4, 2)), dict(alibi_slopes=orc.alibi_slopes(H), attn_mask=m)):
+        full = orc.closed_form(q, k, v, **kw)
+        pos = [3, 17, 39]
+        part = orc.closed_form(q[:, pos], k, v, row_pos=pos, **kw)
+        assert np.allclose(part, full[:, pos], rtol=1e-12, atol=1e-12)
