@@ -5,11 +5,12 @@
 
 #include <cstdint>
 
+#include "common.h"
 #include "trinix_attn.h"
 
 namespace {
 
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
+using trinix::f32x4_t;
 
 // One workgroup per (head, query row); each thread writes runs of 4 keys.
 __global__ __launch_bounds__(256) void alibi_bias_kernel(const float* __restrict__ slopes, int64_t sl_stride,
@@ -40,8 +41,8 @@ extern "C" int trinix_alibi_bias(const float* slopes, int64_t slope_stride, int6
   if (!slopes || !out) return TRINIX_ERR_NULL_POINTER;
   if (nheads <= 0 || seqlen <= 0 || seqlen >= (1ll << 24) || nheads * seqlen >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
   const int vec4 = seqlen % 4 == 0 && out_stride_i % 4 == 0 && out_stride_h % 4 == 0 && ((uintptr_t)out & 15) == 0;
-  (void)hipGetLastError();
-  hipLaunchKernelGGL(alibi_bias_kernel, dim3((unsigned)(nheads * seqlen)), dim3(256), 0, (hipStream_t)stream, slopes,
-                     slope_stride, seqlen, out, out_stride_h, out_stride_i, vec4);
-  return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+  const hipError_t err = trinix::launch_kernel(alibi_bias_kernel, dim3((unsigned)(nheads * seqlen)), dim3(256), 0,
+                                       (hipStream_t)stream, slopes, slope_stride, seqlen, out, out_stride_h,
+                                       out_stride_i, vec4);
+  return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }

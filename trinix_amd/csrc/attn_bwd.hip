@@ -40,11 +40,11 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const uint16_t* __restri
 }
 
 template <class E, int D>
-void launch_delta(const BwdParams& p, hipStream_t st) {
+hipError_t launch_delta(const BwdParams& p, hipStream_t st) {
   constexpr int RPB = 256 / (D / 8);
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  hipLaunchKernelGGL((bwd_delta_kernel<E, D>), dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st, p.o,
-                     p.o_sb, p.o_ss, p.o_sh, p.dout, p.do_sb, p.do_ss, p.do_sh, p.delta, p.Hq, p.Sq, rows);
+  return launch_kernel(&bwd_delta_kernel<E, D>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st, p.o,
+                       p.o_sb, p.o_ss, p.o_sh, p.dout, p.do_sb, p.do_ss, p.do_sh, p.delta, p.Hq, p.Sq, rows);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -152,22 +152,19 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0);
 
   hipStream_t st = (hipStream_t)stream;
-  (void)hipGetLastError();
   hipError_t err;
   if (a->dtype == TRINIX_F32 || a->head_dim == 256 || p.use_dropout) {
+    if (!bwd_generic_fits(p)) return TRINIX_ERR_BAD_SHAPE;
     err = launch_bwd_generic(p, a->dtype, (int)a->head_dim, st);
-    if (err == hipErrorInvalidValue) return TRINIX_ERR_BAD_SHAPE;
     return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
   }
   const bool bf = a->dtype == TRINIX_BF16;
   if (a->head_dim == 128) {
-    if (bf) launch_delta<BF16, 128>(p, st);
-    else launch_delta<F16, 128>(p, st);
-    err = bf ? launch_bwd16_bf16_d128(p, feat, st) : launch_bwd16_f16_d128(p, feat, st);
+    err = bf ? launch_delta<BF16, 128>(p, st) : launch_delta<F16, 128>(p, st);
+    if (err == hipSuccess) err = bf ? launch_bwd16_bf16_d128(p, feat, st) : launch_bwd16_f16_d128(p, feat, st);
   } else {
-    if (bf) launch_delta<BF16, 64>(p, st);
-    else launch_delta<F16, 64>(p, st);
-    err = bf ? launch_bwd16_bf16_d64(p, feat, st) : launch_bwd16_f16_d64(p, feat, st);
+    err = bf ? launch_delta<BF16, 64>(p, st) : launch_delta<F16, 64>(p, st);
+    if (err == hipSuccess) err = bf ? launch_bwd16_bf16_d64(p, feat, st) : launch_bwd16_f16_d64(p, feat, st);
   }
   return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }

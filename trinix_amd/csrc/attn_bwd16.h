@@ -358,8 +358,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
           const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
           x[v] = s[v] * c;
           if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - j);
-          if constexpr (MASK) {
-            if (mcode > 0 && i < p.Sq) x[v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)i * p.mk_si) * kLog2e;
+        }
+        if constexpr (MASK) {
+          // rows vq*8 + 4g + 0..3 of the sub-tile: 4 consecutive rows per
+          // load group, one dtype switch per group (rows past Sq read row
+          // Sq-1; they are masked below)
+          if (mcode > 0) {
+#pragma unroll
+            for (int vq = 0; vq < 4; ++vq) {
+              float mv[4];
+              load_mask4(mrow, p.mask_dtype, i0 + st * 32 + vq * 8 + g * 4, p.mk_si, p.Sq - 1, mv);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x[vq * 4 + e] += mv[e] * kLog2e;
+            }
           }
         }
         if (!full) {
@@ -609,13 +620,26 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
         }
       }
       float x[16];
+      // |i - j| = |fi - (key offset in the block)| with fi = i - n0 - nb*32 - 4g
+      // per tile: the per-element offsets are immediates, so no per-element
+      // value is kept live across tiles
+      const float fi = (float)(i - n0 - nb * 32 - 4 * g);
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int jj = n0 + nb * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
         x[v] = s[v] * c;
-        if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - jj);
-        if constexpr (MASK) {
-          if (mcode > 0 && jj < p.Sk) x[v] += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
+        if constexpr (ALIBI) x[v] += slope_l2 * fabsf(fi - (float)((v >> 2) * 8 + (v & 3)));
+      }
+      if constexpr (MASK) {
+        // keys vq*8 + 4g + 0..3 of the 32-key block: one dtype switch per 4
+        // consecutive keys (keys past Sk read key Sk-1; they are masked below)
+        if (mcode > 0) {
+#pragma unroll
+          for (int vq = 0; vq < 4; ++vq) {
+            float mv[4];
+            load_mask4(mrow, p.mask_dtype, n0 + nb * 32 + vq * 8 + g * 4, p.mk_sj, p.Sk - 1, mv);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[vq * 4 + e] += mv[e] * kLog2e;
+          }
         }
       }
       if (edge) {
@@ -705,16 +729,19 @@ hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
   switch (feat & 3) {
 #define TRINIX_BWD_CASE(F)                                                                                        \
   case F:                                                                                                         \
-    hipLaunchKernelGGL((attn_bwd_dkdv<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_kv, blk_kv, 0, st, p); \
-    hipLaunchKernelGGL((attn_bwd_dq<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>), g_q, blk, 0, st, p);    \
-    return hipGetLastError();
+  {                                                                                                               \
+    const hipError_t e = launch_kernel(&attn_bwd_dkdv<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>, g_kv,   \
+                                       blk_kv, 0, st, p);                                                          \
+    if (e != hipSuccess) return e;                                                                                \
+    return launch_kernel(&attn_bwd_dq<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>, g_q, blk, 0, st, p);     \
+  }
     TRINIX_BWD_CASE(0)
     TRINIX_BWD_CASE(1)
     TRINIX_BWD_CASE(2)
     TRINIX_BWD_CASE(3)
 #undef TRINIX_BWD_CASE
   }
-  return hipErrorInvalidValue;
+  return hipErrorNotSupported;
 }
 
 #define TRINIX_ATTN_BWD16_LAUNCHER(NAME, E, D) \
@@ -729,5 +756,7 @@ hipError_t launch_bwd16_f16_d128(const BwdParams& p, int feat, hipStream_t st);
 // (TRINIX_F32 / F16 / BF16), head_dim 64, 128 or 256, dropout, ALiBi and
 // mask read per element.  Launches its own delta pre-pass.
 hipError_t launch_bwd_generic(const BwdParams& p, int dtype, int D, hipStream_t st);
+// Whether the generic kernels' grids fit 2^31 workgroups.
+bool bwd_generic_fits(const BwdParams& p);
 
 }  // namespace trinix

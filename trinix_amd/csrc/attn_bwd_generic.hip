@@ -376,12 +376,13 @@ __global__ __launch_bounds__(D, 1) void bwd_dq_generic(const BwdParams p) {
 template <class T, int D>
 hipError_t launch_generic(const BwdParams& p, hipStream_t st) {
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
-  hipLaunchKernelGGL((bwd_delta_generic<T, D>), dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, p, rows);
+  hipError_t err = launch_kernel(&bwd_delta_generic<T, D>, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st, p,
+                                 rows);
   const int64_t nkv = (int64_t)p.B * p.Hkv * ((p.Sk + kBT - 1) / kBT);
   const int64_t nq = (int64_t)p.B * p.Hq * ((p.Sq + kBT - 1) / kBT);
-  hipLaunchKernelGGL((bwd_dkdv_generic<T, D>), dim3((unsigned)nkv), dim3(D), 0, st, p);
-  hipLaunchKernelGGL((bwd_dq_generic<T, D>), dim3((unsigned)nq), dim3(D), 0, st, p);
-  return hipGetLastError();
+  if (err == hipSuccess) err = launch_kernel(&bwd_dkdv_generic<T, D>, dim3((unsigned)nkv), dim3(D), 0, st, p);
+  if (err == hipSuccess) err = launch_kernel(&bwd_dq_generic<T, D>, dim3((unsigned)nq), dim3(D), 0, st, p);
+  return err;
 }
 
 template <class T>
@@ -391,22 +392,24 @@ hipError_t launch_generic_d(const BwdParams& p, int D, hipStream_t st) {
     case 128: return launch_generic<T, 128>(p, st);
     case 256: return launch_generic<T, 256>(p, st);
   }
-  return hipErrorInvalidValue;
+  return hipErrorNotSupported;
 }
 
 }  // namespace
 
-hipError_t launch_bwd_generic(const BwdParams& p, int dtype, int D, hipStream_t st) {
+bool bwd_generic_fits(const BwdParams& p) {
   const int64_t nkv = (int64_t)p.B * p.Hkv * ((p.Sk + kBT - 1) / kBT);
   const int64_t nq = (int64_t)p.B * p.Hq * ((p.Sq + kBT - 1) / kBT);
-  if (nkv >= (1ll << 31) || nq >= (1ll << 31) || ((int64_t)p.B * p.Hq * p.Sq + 3) / 4 >= (1ll << 31))
-    return hipErrorInvalidValue;
+  return nkv < (1ll << 31) && nq < (1ll << 31) && ((int64_t)p.B * p.Hq * p.Sq + 3) / 4 < (1ll << 31);
+}
+
+hipError_t launch_bwd_generic(const BwdParams& p, int dtype, int D, hipStream_t st) {
   switch (dtype) {
     case TRINIX_F32: return launch_generic_d<float>(p, D, st);
     case TRINIX_BF16: return launch_generic_d<BF16>(p, D, st);
     case TRINIX_F16: return launch_generic_d<F16>(p, D, st);
   }
-  return hipErrorInvalidValue;
+  return hipErrorNotSupported;
 }
 
 }  // namespace trinix

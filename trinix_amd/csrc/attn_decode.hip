@@ -365,18 +365,17 @@ __global__ __launch_bounds__(256) void attn_decode_combine(DecParams p) {
 template <class E, int D>
 hipError_t launch_decode(const DecParams& p, int feat, hipStream_t st) {
   const dim3 grid((unsigned)((int64_t)p.B * p.Hkv * p.RG * p.n_splits)), block(256);
+  hipError_t err;
   switch (feat) {
-    case 0: hipLaunchKernelGGL((attn_decode16<E, D, false, false>), grid, block, 0, st, p); break;
-    case kFeatAlibi: hipLaunchKernelGGL((attn_decode16<E, D, true, false>), grid, block, 0, st, p); break;
-    case kFeatMask: hipLaunchKernelGGL((attn_decode16<E, D, false, true>), grid, block, 0, st, p); break;
-    case kFeatAlibi | kFeatMask: hipLaunchKernelGGL((attn_decode16<E, D, true, true>), grid, block, 0, st, p); break;
-    default: return hipErrorInvalidValue;
+    case 0: err = launch_kernel(&attn_decode16<E, D, false, false>, grid, block, 0, st, p); break;
+    case kFeatAlibi: err = launch_kernel(&attn_decode16<E, D, true, false>, grid, block, 0, st, p); break;
+    case kFeatMask: err = launch_kernel(&attn_decode16<E, D, false, true>, grid, block, 0, st, p); break;
+    case kFeatAlibi | kFeatMask: err = launch_kernel(&attn_decode16<E, D, true, true>, grid, block, 0, st, p); break;
+    default: return hipErrorNotSupported;
   }
-  hipError_t err = hipGetLastError();
   if (err != hipSuccess || p.n_splits == 1) return err;
   const int64_t rows = (int64_t)p.B * p.Hkv * p.M;
-  hipLaunchKernelGGL((attn_decode_combine<E, D>), dim3((unsigned)rows), dim3(256), 0, st, p);
-  return hipGetLastError();
+  return launch_kernel(&attn_decode_combine<E, D>, dim3((unsigned)rows), dim3(256), 0, st, p);
 }
 
 // Split plan of a decode-shaped forward; false if the split-KV kernel does
@@ -499,7 +498,6 @@ int launch_splitkv(const trinix_attn_fwd_args* a, const SplitPlan& pl, void* wor
   p.part_lse = pl.ws_bytes > 0 ? (float*)workspace + nrows * a->head_dim : nullptr;
   const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0);
 
-  (void)hipGetLastError();
   hipError_t err;
   if (a->dtype == TRINIX_BF16)
     err = a->head_dim == 128 ? launch_decode<BF16, 128>(p, feat, st) : launch_decode<BF16, 64>(p, feat, st);

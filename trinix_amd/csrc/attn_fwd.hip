@@ -9,6 +9,7 @@
 // sums) with one 32-key tile at a time and K/V row-major in LDS; it follows
 // the same semantics and work decomposition as the 16-bit kernel
 // (reference trinix/kernels/attention_kernel.py:123-216, :341-416).
+#include <atomic>
 #include <cstring>
 
 #include <cstdio>
@@ -361,13 +362,20 @@ const char* trinix_status_string(int status) {
 }
 
 int trinix_attn_is_available(void) {
-  int n = 0;
-  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return 0;
+  // The architecture of each device is read once and kept (0 = not read yet,
+  // 1 = not gfx950, 2 = gfx950); later calls cost one hipGetDevice.
+  static std::atomic<int> arch_ok[64];
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < 64) {
+    const int known = arch_ok[dev].load(std::memory_order_relaxed);
+    if (known) return known == 2 ? 1 : 0;
+  }
   hipDeviceProp_t prop;
   if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
-  return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  const int ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+  if (dev < 64) arch_ok[dev].store(ok ? 2 : 1, std::memory_order_relaxed);
+  return ok;
 }
 
 int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* out) {
@@ -452,14 +460,12 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.qn_eps = a->q_norm_eps;
 
   hipStream_t st = (hipStream_t)stream;
-  (void)hipGetLastError();
   hipError_t err;
   if (f32) {
     const dim3 grid((unsigned)p.total_work), block(kWavesF32 * 64);
-    if (a->head_dim == 64) hipLaunchKernelGGL((attn_fwd_f32<64, kWavesF32>), grid, block, 0, st, p);
-    else if (a->head_dim == 128) hipLaunchKernelGGL((attn_fwd_f32<128, kWavesF32>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((attn_fwd_f32<256, kWavesF32>), grid, block, 0, st, p);
-    err = hipGetLastError();
+    if (a->head_dim == 64) err = launch_kernel(&attn_fwd_f32<64, kWavesF32>, grid, block, 0, st, p);
+    else if (a->head_dim == 128) err = launch_kernel(&attn_fwd_f32<128, kWavesF32>, grid, block, 0, st, p);
+    else err = launch_kernel(&attn_fwd_f32<256, kWavesF32>, grid, block, 0, st, p);
   } else {
     const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0) |
                      (p.qn_w ? kFeatQNorm : 0);
@@ -470,7 +476,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
       err = bf ? launch_attn16_bf16_d128(p, cfg, feat, st) : launch_attn16_f16_d128(p, cfg, feat, st);
     else
       err = bf ? launch_attn16_bf16_d256(p, cfg, feat, st) : launch_attn16_f16_d256(p, cfg, feat, st);
-    if (err == hipErrorInvalidValue) return TRINIX_ERR_BAD_ARGUMENT;  // tile config not built
+    if (err == hipErrorNotSupported) return TRINIX_ERR_BAD_ARGUMENT;  // tile config not built
   }
   return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }

@@ -348,8 +348,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
   // Seed of the S^T accumulators: bias / c of ALiBi (element (nb, vq*4 + e)
   // is key n0 + nb*32 + vq*8 + 4g + e of row i), else 0.
+  // At D = 256 with a mask the seeds are added after the QK products instead
+  // (add_alibi): a seeded accumulator keeps the seeds and the products in
+  // separate registers for a moment, which that variant cannot afford.
+  constexpr bool ALIBI_SEED = ALIBI && !(D == 256 && MASK);
   auto seed_scores = [&](int n0, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
-    if constexpr (ALIBI) {
+    if constexpr (ALIBI_SEED) {
       const float fi = (float)(i - n0 - 4 * g);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -361,7 +365,19 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) s[nb] = (f32x16_t){};
     }
+  };  auto add_alibi = [&](int n0, f32x16_t(&s)[NB]) __attribute__((always_inline)) {
+    if constexpr (ALIBI && !ALIBI_SEED) {
+      const float fi = (float)(i - n0 - 4 * g);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            s[nb][vq * 4 + e] = __builtin_fmaf(fabsf(fi - (float)(nb * 32 + vq * 8 + e)), alibi_seed_mul, s[nb][vq * 4 + e]);
+    }
   };
+
 
   // S^T = K Q^T for one tile (keys nb*32 + MFMA row, queries on columns).
   // K fragments are read KPF MFMAs ahead; the sched_group_barriers keep the
@@ -369,7 +385,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   constexpr int NQK = NB * DS;
   // mask kernels (and D = 256, with 192 registers of Q and O) hold more live
   // values: shorter read-ahead
-  constexpr int KPF = D == 256 ? 2 : (MASK && D > 64 ? 3 : 6);
+  constexpr int KPF = D == 256 ? (MASK ? 1 : 2) : (MASK && D > 64 ? (DROP ? 2 : 3) : 6);
   // Byte offset of K fragment (nb, ds) of this lane in a K tile: row
   // nb*32 + r, unit (2ds + g) ^ swz_k(r) (the swizzle depends only on r).  As
   // 16*((2ds) ^ (g ^ swz)) = 32*ds ^ 16*(g ^ swz) and the row offset has no
@@ -398,6 +414,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
       if (k + KPF < NQK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     }
+    add_alibi(n0, s);
   };
 
   // O^T += V^T P^T: the A operand (8 keys of one head_dim row per lane) comes
@@ -431,7 +448,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
   constexpr int NPV = DB * NB * 2;
-  constexpr int VPF = D == 256 ? 2 : (MASK && D > 64 ? 2 : 4);
+  constexpr int VPF = D == 256 ? (MASK ? 1 : 2) : (MASK && D > 64 ? (DROP ? 1 : 2) : 4);
   // vpre: the first VPF fragments, read ahead (before the softmax) by the caller.
   auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2], const u32x4_t(&vpre)[VPF]) __attribute__((always_inline)) {
     u32x4_t vf[NPV];
@@ -473,6 +490,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
             load_mask4(mrow, p.mask_dtype, n0 + nb * 32 + vq * 8 + g * 4, p.mk_sj, p.Sk - 1, mv);
 #pragma unroll
             for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = __builtin_fmaf(mv[e], mscale, s[nb][vq * 4 + e]);
+            // D = 256 (every register in use) or with dropout: one group of
+            // mask values in flight at a time, or their loads are hoisted
+            // together and the kernel spills
+            if constexpr (D == 256 || DROP) __builtin_amdgcn_sched_barrier(0);
           }
       }
     }
@@ -526,6 +547,9 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
           dropout_group(x, p, b * p.Hq + hq, i, n0 + nb * 32 + vq * 8 + g * 4);
 #pragma unroll
           for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = x[e];
+          // with a mask too, one Philox group at a time (interleaved groups
+          // need more registers than the kernel has)
+          if constexpr (MASK) __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll
@@ -660,21 +684,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   }
 
   // Epilogue: O = acc / l (NaN for rows with no allowed key, like the eager
-  // softmax over an all -inf row), optional log-sum-exp.
+  // softmax over an all -inf row), optional log-sum-exp.  The row and lane
+  // indices are passed through empty asm so that the compiler forms the
+  // output addresses here rather than keeping prologue values (64-bit row
+  // offsets) live across the loop, where the mask / dropout / ALiBi
+  // variants have no registers to spare.
+  int ie = i, ge = g;
+  asm volatile("" : "+v"(ie), "+v"(ge));
   const float l = xlane_sum(l_run);
-  if (i < p.Sq && kp == 0) {
+  if (ie < p.Sq && kp == 0) {
     const float inv = 1.f / l;
-    uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)i * p.o_ss;
+    uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)ie * p.o_ss;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int vq = 0; vq < 4; ++vq) {
-        const int d0 = db * 32 + vq * 8 + g * 4;
+        const int d0 = db * 32 + vq * 8 + ge * 4;
         const u32x2_t w2 = {E::pack(acc[db][vq * 4 + 0] * inv, acc[db][vq * 4 + 1] * inv),
                             E::pack(acc[db][vq * 4 + 2] * inv, acc[db][vq * 4 + 3] * inv)};
         *(u32x2_t*)(orow + d0) = w2;
       }
-    if (p.lse && g == 0) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = (m_run + __log2f(l)) * kLn2;
+    if (p.lse && ge == 0) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + ie] = (m_run + __log2f(l)) * kLn2;
   }
 }
 
@@ -685,10 +715,9 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   switch (feat) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
-    hipLaunchKernelGGL((attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,     \
-                                        (F & kFeatDropout) != 0, (F & kFeatQNorm) != 0>),                       \
-                       grid, block, 0, st, p);                                                                  \
-    return hipGetLastError();
+    return launch_kernel(&attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,  \
+                                          (F & kFeatDropout) != 0, (F & kFeatQNorm) != 0>,                     \
+                         grid, block, 0, st, p);
     TRINIX_CASE(0)
     TRINIX_CASE(1)
     TRINIX_CASE(2)
@@ -712,7 +741,7 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
     }
   }
 #undef TRINIX_CASE
-  return hipErrorInvalidValue;
+  return hipErrorNotSupported;
 }
 
 // Tile configs built per (dtype, D), every feature combination:
@@ -724,11 +753,11 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
 #define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                                   \
   hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                                \
     constexpr int kOcc = (D) == 256 ? 1 : 2;                                                               \
-    if (cfg.bn != 64 || cfg.nw != 4 || cfg.occ != kOcc) return hipErrorInvalidValue;                       \
+    if (cfg.bn != 64 || cfg.nw != 4 || cfg.occ != kOcc) return hipErrorNotSupported;                       \
     if (cfg.ks == 1) return launch_feat<E, D, 64, 4, kOcc, 1>(p, feat, st);                                \
     if constexpr ((D) == 64)                                                                               \
       if (cfg.ks == 2) return launch_feat<E, D, 64, 4, kOcc, 2>(p, feat, st);                              \
-    return hipErrorInvalidValue;                                                                             \
+    return hipErrorNotSupported;                                                                             \
   }
 
 }  // namespace trinix

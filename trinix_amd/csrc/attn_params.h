@@ -108,7 +108,7 @@ __device__ inline float xlane_sum(float x) {
 __device__ inline bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
 
 // Launchers of the 16-bit kernels, one translation unit per (dtype, D).
-// Return hipErrorInvalidValue for a (cfg, features) pair not instantiated.
+// Return hipErrorNotSupported for a (cfg, features) pair not instantiated.
 hipError_t launch_attn16_bf16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 hipError_t launch_attn16_bf16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 hipError_t launch_attn16_f16_d64(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);

@@ -5,7 +5,28 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <tuple>
+#include <type_traits>
+#include <utility>
+
 namespace trinix {
+
+// Launches `kernel` on `st` through hipLaunchKernel and returns the status of
+// this launch alone.  hipGetLastError is never called, so an error an
+// earlier call left for the caller stays there for the caller to read.
+// Arguments are converted to the kernel's parameter types first.
+template <typename... KArgs, typename... Args>
+inline hipError_t launch_kernel(void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem, hipStream_t st,
+                                Args&&... args) {
+  static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count");
+  std::tuple<std::decay_t<KArgs>...> vals(static_cast<std::decay_t<KArgs>>(std::forward<Args>(args))...);
+  return std::apply(
+      [&](auto&... v) {
+        void* ptrs[] = {static_cast<void*>(&v)...};
+        return hipLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, shmem, st);
+      },
+      vals);
+}
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));

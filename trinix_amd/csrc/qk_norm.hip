@@ -119,17 +119,17 @@ extern "C" int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* ou
   const int64_t blocks = (threads + 255) / 256;
   if (blocks >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
   hipStream_t st = (hipStream_t)stream;
-  (void)hipGetLastError();
   const dim3 grid((unsigned)blocks), block(256);
+  hipError_t err;
   if (dtype == TRINIX_BF16)
-    hipLaunchKernelGGL(qk_norm_kernel<BF16>, grid, block, 0, st, (const uint16_t*)x, x_stride[0], x_stride[1],
+    err = launch_kernel(&qk_norm_kernel<BF16>, grid, block, 0, st, (const uint16_t*)x, x_stride[0], x_stride[1],
                        x_stride[2], (uint16_t*)out, out_stride[0], out_stride[1], out_stride[2], (int)seqlen,
                        (int)nheads, (int)head_dim, (const uint16_t*)weight, eps, (const uint16_t*)cos,
                        (const uint16_t*)sin, cs_stride, cs_rows, position_ids, rows);
   else
-    hipLaunchKernelGGL(qk_norm_kernel<F16>, grid, block, 0, st, (const uint16_t*)x, x_stride[0], x_stride[1],
+    err = launch_kernel(&qk_norm_kernel<F16>, grid, block, 0, st, (const uint16_t*)x, x_stride[0], x_stride[1],
                        x_stride[2], (uint16_t*)out, out_stride[0], out_stride[1], out_stride[2], (int)seqlen,
                        (int)nheads, (int)head_dim, (const uint16_t*)weight, eps, (const uint16_t*)cos,
                        (const uint16_t*)sin, cs_stride, cs_rows, position_ids, rows);
-  return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+  return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }

@@ -204,7 +204,7 @@ int trinix_rope_apply(const void* x, const int64_t xs[4], void* out, const int64
   if (xs[3] != 1 || os[3] != 1) return TRINIX_ERR_BAD_STRIDE;
   if (seqlen >= (1ll << 31) || batch >= (1ll << 31) || nheads >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
   hipStream_t st = (hipStream_t)stream;
-  (void)hipGetLastError();
+  hipError_t err;
   const int S = (int)seqlen, H = (int)nheads, D = (int)head_dim;
   const bool vec = dtype != TRINIX_F32 && D % 16 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 &&
                    ((uintptr_t)cosp & 15) == 0 && ((uintptr_t)sinp & 15) == 0 && cs % 8 == 0 &&
@@ -214,11 +214,11 @@ int trinix_rope_apply(const void* x, const int64_t xs[4], void* out, const int64
     const int64_t total = batch * seqlen * nheads * (D / 16);
     const dim3 grid((unsigned)((total + 255) / 256));
     if (dtype == TRINIX_BF16)
-      hipLaunchKernelGGL(rope16_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t*)x, xs[0], xs[1], xs[2],
+      err = launch_kernel(&rope16_kernel<BF16>, grid, dim3(256), 0, st, (const uint16_t*)x, xs[0], xs[1], xs[2],
                          (uint16_t*)out, os[0], os[1], os[2], S, H, D, (const uint16_t*)cosp,
                          (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else if (dtype == TRINIX_F16)
-      hipLaunchKernelGGL(rope16_kernel<F16>, grid, dim3(256), 0, st, (const uint16_t*)x, xs[0], xs[1], xs[2],
+      err = launch_kernel(&rope16_kernel<F16>, grid, dim3(256), 0, st, (const uint16_t*)x, xs[0], xs[1], xs[2],
                          (uint16_t*)out, os[0], os[1], os[2], S, H, D, (const uint16_t*)cosp,
                          (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else
@@ -227,21 +227,21 @@ int trinix_rope_apply(const void* x, const int64_t xs[4], void* out, const int64
     const int64_t total = batch * seqlen * nheads * (D / 2);
     const dim3 grid((unsigned)((total + 255) / 256));
     if (dtype == TRINIX_BF16)
-      hipLaunchKernelGGL((rope_scalar_kernel<BF16Scalar, uint16_t>), grid, dim3(256), 0, st, (const uint16_t*)x,
+      err = launch_kernel(&rope_scalar_kernel<BF16Scalar, uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)x,
                          xs[0], xs[1], xs[2], (uint16_t*)out, os[0], os[1], os[2], S, H, D,
                          (const uint16_t*)cosp, (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else if (dtype == TRINIX_F16)
-      hipLaunchKernelGGL((rope_scalar_kernel<F16Scalar, uint16_t>), grid, dim3(256), 0, st, (const uint16_t*)x,
+      err = launch_kernel(&rope_scalar_kernel<F16Scalar, uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)x,
                          xs[0], xs[1], xs[2], (uint16_t*)out, os[0], os[1], os[2], S, H, D,
                          (const uint16_t*)cosp, (const uint16_t*)sinp, cs, cs_rows, position_ids, total);
     else if (dtype == TRINIX_F32)
-      hipLaunchKernelGGL((rope_scalar_kernel<F32Scalar, float>), grid, dim3(256), 0, st, (const float*)x, xs[0],
+      err = launch_kernel(&rope_scalar_kernel<F32Scalar, float>, grid, dim3(256), 0, st, (const float*)x, xs[0],
                          xs[1], xs[2], (float*)out, os[0], os[1], os[2], S, H, D, (const float*)cosp,
                          (const float*)sinp, cs, cs_rows, position_ids, total);
     else
       return TRINIX_ERR_BAD_DTYPE;
   }
-  return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+  return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }
 
 int trinix_attn_mask_blockmap(const void* mask, int32_t mask_dtype, int64_t mb, int64_t mh, int64_t seqlen_q,
@@ -263,11 +263,10 @@ int trinix_attn_mask_blockmap(const void* mask, int32_t mask_dtype, int64_t mb, 
   const int vec = stride[3] == 1 && ((uintptr_t)mask % align) == 0 && aligned(stride[0], mb) &&
                   aligned(stride[1], mh) && aligned(stride[2], seqlen_q);
   hipStream_t st = (hipStream_t)stream;
-  (void)hipGetLastError();
-  hipLaunchKernelGGL(blockmap_kernel, dim3(cols, rows, (unsigned)(mb * mh)), dim3(256), 0, st, (const char*)mask,
-                     (int)mask_dtype, stride[0], stride[1], stride[2], stride[3], (int)mh, (int)seqlen_q,
-                     (int)seqlen_k, rows, cols, vec, out);
-  return hipGetLastError() == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+  const hipError_t err = launch_kernel(&blockmap_kernel, dim3(cols, rows, (unsigned)(mb * mh)), dim3(256), 0, st,
+                                       (const char*)mask, (int)mask_dtype, stride[0], stride[1], stride[2], stride[3],
+                                       (int)mh, (int)seqlen_q, (int)seqlen_k, rows, cols, vec, out);
+  return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
 }
 
 }  // extern "C"
