@@ -62,6 +62,11 @@ def sources() -> list[Path]:
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
+def host_sources() -> list[Path]:
+    """Plain C++ host code (argument checks, launch planning), compiled by g++."""
+    return sorted(CSRC_DIR.glob("*.cpp"))
+
+
 def _compile_flags() -> list[str]:
     return [*HIPCC_FLAGS, f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}"]
 
@@ -129,6 +134,15 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     cflags += ["-Rpass-analysis=kernel-resource-usage", "-save-temps=obj"]
     srcs = sources()
     objs = [obj_dir / (s.stem + ".o") for s in srcs]
+    host_objs = [obj_dir / (s.stem + ".host.o") for s in host_sources()]
+    for src, obj in zip(host_sources(), host_objs):
+        cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-Wall", f"-I{INCLUDE_DIR}", f"-I{CSRC_DIR}", "-c", str(src),
+               "-o", str(obj)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"g++ failed on {src.name}:\n{res.stderr[-6000:]}")
     jobs = jobs or max(1, min(len(srcs), os.cpu_count() or 1, 8))
     pending = list(zip(srcs, objs))
     running = []
@@ -159,7 +173,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if bad:
         raise RuntimeError("kernels spill registers to memory or to accumulation registers:\n" + "\n".join(bad))
     tmp = LIB_DIR / (LIB_NAME + f".tmp{os.getpid()}")
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), *map(str, host_objs), "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

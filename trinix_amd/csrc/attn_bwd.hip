@@ -9,6 +9,7 @@
 #include <cstdint>
 
 #include "attn_bwd16.h"
+#include "host_plan.h"
 
 namespace trinix {
 namespace {
@@ -47,52 +48,14 @@ hipError_t launch_delta(const BwdParams& p, hipStream_t st) {
                        p.o_sb, p.o_ss, p.o_sh, p.dout, p.do_sb, p.do_ss, p.do_sh, p.delta, p.Hq, p.Sq, rows);
 }
 
-bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
-
-// fp32 BSHD tensor (generic kernels, element loads): head_dim stride 1.
-int check32(const void* ptr, const int64_t st[4]) {
-  if (!ptr) return TRINIX_ERR_NULL_POINTER;
-  if (st[3] != 1 || ((uintptr_t)ptr & 3) != 0) return TRINIX_ERR_BAD_STRIDE;
-  return TRINIX_OK;
-}
-
-// 16-bit BSHD tensor: head_dim stride 1, 16-byte aligned rows, and a row
-// stride the 32-bit in-tile offsets can address (tiles of up to 128 rows).
-int check16(const void* ptr, const int64_t st[4]) {
-  if (!ptr) return TRINIX_ERR_NULL_POINTER;
-  if (st[3] != 1 || !aligned16(ptr)) return TRINIX_ERR_BAD_STRIDE;
-  for (int a = 0; a < 3; ++a)
-    if (st[a] % 8 != 0) return TRINIX_ERR_BAD_STRIDE;
-  if (st[1] < 0 || st[1] >= (1ll << 22)) return TRINIX_ERR_BAD_STRIDE;
-  return TRINIX_OK;
-}
-
 }  // namespace
 }  // namespace trinix
 
 using namespace trinix;
 
 extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
-  if (!a) return TRINIX_ERR_NULL_POINTER;
-  if (a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F32) return TRINIX_ERR_BAD_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
-  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
-  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0 ||
-      a->nheads_q % a->nheads_kv != 0)
-    return TRINIX_ERR_BAD_SHAPE;
-  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
-    return TRINIX_ERR_BAD_SHAPE;
-  if (!a->lse || !a->delta) return TRINIX_ERR_NULL_POINTER;
-  int rc;
-  auto check = a->dtype == TRINIX_F32 ? check32 : check16;
-  if ((rc = check(a->q, a->q_stride)) || (rc = check(a->k, a->k_stride)) || (rc = check(a->v, a->v_stride)) ||
-      (rc = check(a->out, a->out_stride)) || (rc = check(a->dout, a->dout_stride)) ||
-      (rc = check(a->dq, a->dq_stride)) || (rc = check(a->dk, a->dk_stride)) || (rc = check(a->dv, a->dv_stride)))
-    return rc;
-  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
-      a->mask_dtype != TRINIX_U8)
-    return TRINIX_ERR_BAD_DTYPE;
-  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+  const int vrc = validate_bwd_args(a);
+  if (vrc != TRINIX_OK) return vrc;
 
   BwdParams p;
   p.q = (const uint16_t*)a->q;

@@ -28,6 +28,7 @@
 #include <type_traits>
 
 #include "attn_params.h"
+#include "host_plan.h"
 
 namespace trinix {
 
@@ -58,9 +59,6 @@ struct DecParams {
   float* part_lse;      // (B*Hkv*M, n_splits) log2-domain partial lse
 };
 
-constexpr int kDecodeMaxSq = 16;
-constexpr int kDecodeTargetWgs = 1024;  // 4 workgroups of 4 wavefronts per CU
-constexpr int kDecodeMinChunk = 128;
 
 template <class E, int D, bool ALIBI, bool MASK>
 __global__ __launch_bounds__(256) void attn_decode16(DecParams p) {
@@ -376,62 +374,6 @@ hipError_t launch_decode(const DecParams& p, int feat, hipStream_t st) {
   if (err != hipSuccess || p.n_splits == 1) return err;
   const int64_t rows = (int64_t)p.B * p.Hkv * p.M;
   return launch_kernel(&attn_decode_combine<E, D>, dim3((unsigned)rows), dim3(256), 0, st, p);
-}
-
-// Split plan of a decode-shaped forward; false if the split-KV kernel does
-// not apply (then trinix_attn_fwd is the path).
-struct SplitPlan {
-  int n_splits, chunk, klo, khi, M, RG;
-  int64_t ws_bytes;
-};
-
-bool make_split_plan(const trinix_attn_fwd_args* a, SplitPlan* pl) {
-  if (a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F16) return false;
-  if (a->dropout_p > 0.f || a->rope_cos || a->q_norm_weight) return false;
-  if (a->seqlen_q > kDecodeMaxSq) return false;
-  if (a->head_dim != 64 && a->head_dim != 128) return false;
-  const int64_t Sq = a->seqlen_q, Sk = a->seqlen_k;
-  const int64_t G = a->nheads_q / a->nheads_kv;
-  const int64_t M = G * Sq;
-  const int64_t RG = (M + 15) / 16;
-  const int64_t lim = 1ll << 40;
-  const int64_t wl = a->window_left < -lim ? -lim : (a->window_left > lim ? lim : a->window_left);
-  const int64_t wr = a->window_right < -lim ? -lim : (a->window_right > lim ? lim : a->window_right);
-  // Keys some row i in [0, Sq) may see: lo(i) = max(0, i - wl) is smallest at
-  // i = 0, hi(i) = min(Sk - 1, i (causal), i + wr (window)) largest at Sq - 1.
-  int64_t klo = a->has_window ? -wl : 0;
-  klo = klo < 0 ? 0 : (klo > Sk ? Sk : klo);
-  int64_t hi = Sk - 1;
-  if (a->causal) hi = hi < Sq - 1 ? hi : Sq - 1;
-  if (a->has_window) hi = hi < Sq - 1 + wr ? hi : Sq - 1 + wr;
-  int64_t khi = hi + 1;
-  khi = khi < 0 ? 0 : (khi > Sk ? Sk : khi);
-  if (khi <= klo) return false;  // no visible key: every row is NaN, leave it to trinix_attn_fwd
-  const int64_t span = khi - klo;
-  const int64_t items = a->batch * a->nheads_kv * RG;
-  int64_t target = kDecodeTargetWgs, min_chunk = kDecodeMinChunk;
-  if (const char* env = getenv("TRINIX_SPLITKV_CFG")) {  // "target_wgs,min_chunk" (tuning only)
-    long long t = 0, c = 0;
-    if (sscanf(env, "%lld,%lld", &t, &c) == 2 && t > 0 && c >= 64) {
-      target = t;
-      min_chunk = c;
-    }
-  }
-  const int64_t max_splits = (span + min_chunk - 1) / min_chunk;
-  int64_t n = (target + items - 1) / items;
-  n = n < 1 ? 1 : (n > max_splits ? max_splits : n);
-  int64_t chunk = (span + n - 1) / n;
-  chunk = (chunk + 63) / 64 * 64;
-  n = (span + chunk - 1) / chunk;
-  if (items * n >= (1ll << 31)) return false;
-  pl->n_splits = (int)n;
-  pl->chunk = (int)chunk;
-  pl->klo = (int)klo;
-  pl->khi = (int)khi;
-  pl->M = (int)M;
-  pl->RG = (int)RG;
-  pl->ws_bytes = n > 1 ? a->batch * a->nheads_kv * M * n * (a->head_dim + 1) * 4 : 0;
-  return true;
 }
 
 }  // namespace trinix

@@ -16,6 +16,7 @@
 #include <cstdlib>
 
 #include "attn_params.h"
+#include "host_plan.h"
 
 namespace trinix {
 
@@ -257,89 +258,7 @@ namespace {
 
 constexpr int kWavesF32 = 4;
 
-bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
-
-constexpr int64_t kMaxKvRowStride = 1ll << 22;  // elements; 128 rows * 2 B * 2^22 = 2^30 bytes
-
-int check_tensor(const void* ptr, const int64_t st[4], int esize) {
-  if (!ptr) return TRINIX_ERR_NULL_POINTER;
-  if (st[3] != 1) return TRINIX_ERR_BAD_STRIDE;
-  if (esize == 2) {
-    // 16-byte vector loads of 8 consecutive head_dim elements per row
-    if (!aligned16(ptr)) return TRINIX_ERR_BAD_STRIDE;
-    for (int a = 0; a < 3; ++a)
-      if (st[a] % 8 != 0) return TRINIX_ERR_BAD_STRIDE;
-  } else if (((uintptr_t)ptr & 3) != 0) {
-    return TRINIX_ERR_BAD_STRIDE;
-  }
-  return TRINIX_OK;
-}
-
-// Tile configuration of the 16-bit kernel: 4 wavefronts x 32 query rows,
-// 64-key tiles, 2 wavefronts per SIMD (1 for head_dim 256).  A small grid at
-// head_dim 64 -- no more 128-row workgroups than CUs -- splits each 32-row
-// group's keys between two wavefronts (ks = 2, 64 rows per workgroup): twice
-// the workgroups, half the longest chain of tiles, at twice the K/V copies
-// per flop.  Measured at head_dim 64, bf16: 128 workgroups at S = 4096..16384
-// +50..62%, 64 workgroups at S = 1024 +2%, 384 workgroups (S = 1024) -3%.
-// TRINIX_ATTN_CFG="nw,occ,bn[,ks]" overrides the choice (tuning only; a
-// configuration that is not built is rejected with TRINIX_ERR_BAD_ARGUMENT).
-constexpr int64_t kSmallGrid = 256;  // CUs of an MI355X
-Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq) {
-  Cfg16 c{4, head_dim == 256 ? 1 : 2, 64, 1};
-  if (head_dim == 64 && batch * hq * ((sq + 127) / 128) <= kSmallGrid) c.ks = 2;
-  if (const char* env = getenv("TRINIX_ATTN_CFG")) {
-    int nw = 0, occ = 0, bn = 0, ks = 1;
-    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &ks) >= 3 && nw > 0 && ks > 0 && nw % ks == 0)
-      c = Cfg16{nw, occ, bn, ks};
-  }
-  return c;
-}
-
 }  // namespace
-
-namespace trinix {
-
-int validate_fwd_args(const trinix_attn_fwd_args* a) {
-  if (!a) return TRINIX_ERR_NULL_POINTER;
-  const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
-  if (a->dtype != TRINIX_F32 && a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
-  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
-  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0)
-    return TRINIX_ERR_BAD_SHAPE;
-  if (a->nheads_q % a->nheads_kv != 0) return TRINIX_ERR_BAD_SHAPE;
-  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
-    return TRINIX_ERR_BAD_SHAPE;
-  int rc;
-  if ((rc = check_tensor(a->q, a->q_stride, esize))) return rc;
-  if ((rc = check_tensor(a->k, a->k_stride, esize))) return rc;
-  if ((rc = check_tensor(a->v, a->v_stride, esize))) return rc;
-  // 16-bit kernels address a K/V tile (up to 128 key rows) as one base plus
-  // per-lane 32-bit byte offsets: the key-row stride must be in [0, 2^22).
-  if (esize == 2 && (a->k_stride[1] < 0 || a->k_stride[1] >= kMaxKvRowStride || a->v_stride[1] < 0 ||
-                     a->v_stride[1] >= kMaxKvRowStride))
-    return TRINIX_ERR_BAD_STRIDE;
-  if ((rc = check_tensor(a->out, a->out_stride, esize))) return rc;
-  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
-      a->mask_dtype != TRINIX_U8)
-    return TRINIX_ERR_BAD_DTYPE;
-  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
-  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
-  if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
-  if (a->rope_cos && esize == 2 &&
-      (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
-    return TRINIX_ERR_BAD_STRIDE;
-  if (a->q_norm_weight) {
-    if (esize != 2) return TRINIX_ERR_BAD_DTYPE;
-    if (a->mask || a->dropout_p > 0.f) return TRINIX_ERR_BAD_ARGUMENT;
-    if (!aligned16(a->q_norm_weight)) return TRINIX_ERR_BAD_STRIDE;
-    if (!(a->q_norm_eps >= 0.f)) return TRINIX_ERR_BAD_ARGUMENT;
-  }
-
-  return TRINIX_OK;
-}
-
-}  // namespace trinix
 
 extern "C" {
 

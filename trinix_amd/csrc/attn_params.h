@@ -2,6 +2,7 @@
 // they share (mask element loads, dropout, cross-lane reductions).
 #pragma once
 #include "common.h"
+#include "host_plan.h"
 #include "trinix_attn.h"
 
 namespace trinix {
@@ -40,13 +41,6 @@ struct FwdParams {
   float qn_eps;
 };
 
-// Tile shape of one 16-bit kernel instantiation.
-struct Cfg16 {
-  int nw;   // wavefronts per workgroup (32 query rows per key split)
-  int occ;  // target wavefronts per SIMD (register budget 512 / occ)
-  int bn;   // keys per K/V tile
-  int ks;   // key split: wavefronts sharing one 32-row group (rows per workgroup = 32 * nw / ks)
-};
 
 __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx) {
   switch (dtype) {
@@ -116,9 +110,6 @@ hipError_t launch_attn16_f16_d128(const FwdParams& p, Cfg16 cfg, int feat, hipSt
 hipError_t launch_attn16_bf16_d256(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 hipError_t launch_attn16_f16_d256(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st);
 
-// Host-side argument checks of trinix_attn_fwd (no launch); also applied by
-// the split-KV entry points.
-int validate_fwd_args(const trinix_attn_fwd_args* a);
 
 // Feature bits of a launch (compile-time flags of the 16-bit kernels).
 enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4, kFeatQNorm = 8 };

@@ -1,0 +1,182 @@
+// Host-only argument checks and launch planning (declared in host_plan.h):
+// plain C++, no HIP.  Every function only reads its arguments and returns a
+// status, a plan or a tile shape.
+#include "host_plan.h"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace trinix {
+namespace {
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+int check_tensor(const void* ptr, const int64_t st[4], int esize) {
+  if (!ptr) return TRINIX_ERR_NULL_POINTER;
+  if (st[3] != 1) return TRINIX_ERR_BAD_STRIDE;
+  if (esize == 2) {
+    // 16-byte vector loads of 8 consecutive head_dim elements per row
+    if (!aligned16(ptr)) return TRINIX_ERR_BAD_STRIDE;
+    for (int a = 0; a < 3; ++a)
+      if (st[a] % 8 != 0) return TRINIX_ERR_BAD_STRIDE;
+  } else if (((uintptr_t)ptr & 3) != 0) {
+    return TRINIX_ERR_BAD_STRIDE;
+  }
+  return TRINIX_OK;
+}
+
+// fp32 BSHD tensor (generic kernels, element loads): head_dim stride 1.
+int check32(const void* ptr, const int64_t st[4]) {
+  if (!ptr) return TRINIX_ERR_NULL_POINTER;
+  if (st[3] != 1 || ((uintptr_t)ptr & 3) != 0) return TRINIX_ERR_BAD_STRIDE;
+  return TRINIX_OK;
+}
+
+// 16-bit BSHD tensor: head_dim stride 1, 16-byte aligned rows, and a row
+// stride the 32-bit in-tile offsets can address (tiles of up to 128 rows).
+int check16(const void* ptr, const int64_t st[4]) {
+  if (!ptr) return TRINIX_ERR_NULL_POINTER;
+  if (st[3] != 1 || !aligned16(ptr)) return TRINIX_ERR_BAD_STRIDE;
+  for (int a = 0; a < 3; ++a)
+    if (st[a] % 8 != 0) return TRINIX_ERR_BAD_STRIDE;
+  if (st[1] < 0 || st[1] >= kMaxKvRowStride) return TRINIX_ERR_BAD_STRIDE;
+  return TRINIX_OK;
+}
+
+}  // namespace
+
+// Tile configuration of the 16-bit kernel: 4 wavefronts x 32 query rows,
+// 64-key tiles, 2 wavefronts per SIMD (1 for head_dim 256).  A small grid at
+// head_dim 64 -- no more 128-row workgroups than CUs -- splits each 32-row
+// group's keys between two wavefronts (ks = 2, 64 rows per workgroup): twice
+// the workgroups, half the longest chain of tiles, at twice the K/V copies
+// per flop.  Measured at head_dim 64, bf16: 128 workgroups at S = 4096..16384
+// +50..62%, 64 workgroups at S = 1024 +2%, 384 workgroups (S = 1024) -3%.
+// TRINIX_ATTN_CFG="nw,occ,bn[,ks]" overrides the choice (tuning only; a
+// configuration that is not built is rejected with TRINIX_ERR_BAD_ARGUMENT).
+constexpr int64_t kSmallGrid = 256;  // CUs of an MI355X
+Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq) {
+  Cfg16 c{4, head_dim == 256 ? 1 : 2, 64, 1};
+  // batch * hq * row blocks, without overflow (each factor < 2^31 here)
+  if (head_dim == 64 && batch * hq <= kSmallGrid && batch * hq * ((sq + 127) / 128) <= kSmallGrid) c.ks = 2;
+  if (const char* env = getenv("TRINIX_ATTN_CFG")) {
+    int nw = 0, occ = 0, bn = 0, ks = 1;
+    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &ks) >= 3 && nw > 0 && ks > 0 && nw % ks == 0)
+      c = Cfg16{nw, occ, bn, ks};
+  }
+  return c;
+}
+
+int validate_fwd_args(const trinix_attn_fwd_args* a) {
+  if (!a) return TRINIX_ERR_NULL_POINTER;
+  const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
+  if (a->dtype != TRINIX_F32 && a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16) return TRINIX_ERR_BAD_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0)
+    return TRINIX_ERR_BAD_SHAPE;
+  if (a->nheads_q % a->nheads_kv != 0) return TRINIX_ERR_BAD_SHAPE;
+  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
+    return TRINIX_ERR_BAD_SHAPE;
+  int rc;
+  if ((rc = check_tensor(a->q, a->q_stride, esize))) return rc;
+  if ((rc = check_tensor(a->k, a->k_stride, esize))) return rc;
+  if ((rc = check_tensor(a->v, a->v_stride, esize))) return rc;
+  // 16-bit kernels address a K/V tile (up to 128 key rows) as one base plus
+  // per-lane 32-bit byte offsets: the key-row stride must be in [0, 2^22).
+  if (esize == 2 && (a->k_stride[1] < 0 || a->k_stride[1] >= kMaxKvRowStride || a->v_stride[1] < 0 ||
+                     a->v_stride[1] >= kMaxKvRowStride))
+    return TRINIX_ERR_BAD_STRIDE;
+  if ((rc = check_tensor(a->out, a->out_stride, esize))) return rc;
+  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
+      a->mask_dtype != TRINIX_U8)
+    return TRINIX_ERR_BAD_DTYPE;
+  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
+  if (a->rope_cos && esize == 2 &&
+      (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
+    return TRINIX_ERR_BAD_STRIDE;
+  if (a->q_norm_weight) {
+    if (esize != 2) return TRINIX_ERR_BAD_DTYPE;
+    if (a->mask || a->dropout_p > 0.f) return TRINIX_ERR_BAD_ARGUMENT;
+    if (!aligned16(a->q_norm_weight)) return TRINIX_ERR_BAD_STRIDE;
+    if (!(a->q_norm_eps >= 0.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  }
+
+  return TRINIX_OK;
+}
+
+int validate_bwd_args(const trinix_attn_bwd_args* a) {
+  if (!a) return TRINIX_ERR_NULL_POINTER;
+  if (a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F32) return TRINIX_ERR_BAD_DTYPE;
+  if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
+  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0 ||
+      a->nheads_q % a->nheads_kv != 0)
+    return TRINIX_ERR_BAD_SHAPE;
+  if (a->seqlen_q >= (1ll << 30) || a->seqlen_k >= (1ll << 30) || a->batch >= (1 << 20) || a->nheads_q >= (1 << 20))
+    return TRINIX_ERR_BAD_SHAPE;
+  if (!a->lse || !a->delta) return TRINIX_ERR_NULL_POINTER;
+  int rc;
+  auto check = a->dtype == TRINIX_F32 ? check32 : check16;
+  if ((rc = check(a->q, a->q_stride)) || (rc = check(a->k, a->k_stride)) || (rc = check(a->v, a->v_stride)) ||
+      (rc = check(a->out, a->out_stride)) || (rc = check(a->dout, a->dout_stride)) ||
+      (rc = check(a->dq, a->dq_stride)) || (rc = check(a->dk, a->dk_stride)) || (rc = check(a->dv, a->dv_stride)))
+    return rc;
+  if (a->mask && a->mask_dtype != TRINIX_F32 && a->mask_dtype != TRINIX_F16 && a->mask_dtype != TRINIX_BF16 &&
+      a->mask_dtype != TRINIX_U8)
+    return TRINIX_ERR_BAD_DTYPE;
+  if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+  return TRINIX_OK;
+}
+
+bool make_split_plan(const trinix_attn_fwd_args* a, SplitPlan* pl) {
+  if (a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F16) return false;
+  if (a->dropout_p > 0.f || a->rope_cos || a->q_norm_weight) return false;
+  if (a->seqlen_q > kDecodeMaxSq) return false;
+  if (a->head_dim != 64 && a->head_dim != 128) return false;
+  const int64_t Sq = a->seqlen_q, Sk = a->seqlen_k;
+  const int64_t G = a->nheads_q / a->nheads_kv;
+  const int64_t M = G * Sq;
+  const int64_t RG = (M + 15) / 16;
+  const int64_t lim = 1ll << 40;
+  const int64_t wl = a->window_left < -lim ? -lim : (a->window_left > lim ? lim : a->window_left);
+  const int64_t wr = a->window_right < -lim ? -lim : (a->window_right > lim ? lim : a->window_right);
+  // Keys some row i in [0, Sq) may see: lo(i) = max(0, i - wl) is smallest at
+  // i = 0, hi(i) = min(Sk - 1, i (causal), i + wr (window)) largest at Sq - 1.
+  int64_t klo = a->has_window ? -wl : 0;
+  klo = klo < 0 ? 0 : (klo > Sk ? Sk : klo);
+  int64_t hi = Sk - 1;
+  if (a->causal) hi = hi < Sq - 1 ? hi : Sq - 1;
+  if (a->has_window) hi = hi < Sq - 1 + wr ? hi : Sq - 1 + wr;
+  int64_t khi = hi + 1;
+  khi = khi < 0 ? 0 : (khi > Sk ? Sk : khi);
+  if (khi <= klo) return false;  // no visible key: every row is NaN, leave it to trinix_attn_fwd
+  const int64_t span = khi - klo;
+  const int64_t items = a->batch * a->nheads_kv * RG;
+  int64_t target = kDecodeTargetWgs, min_chunk = kDecodeMinChunk;
+  if (const char* env = getenv("TRINIX_SPLITKV_CFG")) {  // "target_wgs,min_chunk" (tuning only)
+    long long t = 0, c = 0;
+    if (sscanf(env, "%lld,%lld", &t, &c) == 2 && t > 0 && c >= 64) {
+      target = t;
+      min_chunk = c;
+    }
+  }
+  const int64_t max_splits = (span + min_chunk - 1) / min_chunk;
+  int64_t n = (target + items - 1) / items;
+  n = n < 1 ? 1 : (n > max_splits ? max_splits : n);
+  int64_t chunk = (span + n - 1) / n;
+  chunk = (chunk + 63) / 64 * 64;
+  n = (span + chunk - 1) / chunk;
+  if (items * n >= (1ll << 31)) return false;
+  pl->n_splits = (int)n;
+  pl->chunk = (int)chunk;
+  pl->klo = (int)klo;
+  pl->khi = (int)khi;
+  pl->M = (int)M;
+  pl->RG = (int)RG;
+  pl->ws_bytes = n > 1 ? a->batch * a->nheads_kv * M * n * (a->head_dim + 1) * 4 : 0;
+  return true;
+}
+
+}  // namespace trinix
