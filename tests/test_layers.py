@@ -126,3 +126,40 @@ def test_rope_embedding_tables_and_alibi_module():
     b = alibi(5, batch_size=2)
     assert b.shape == (2, 8, 5, 5)
     assert torch.equal(b[0], orc.alibi_bias(5, 5, orc.alibi_slopes(8)))
+
+
+def test_custom_position_module_calling_conventions():
+    """User position modules are called as the reference layers call them
+    (base.py:239-285): the full argument list, else (q, k), else no
+    arguments; results are (q, k, bias), (q, k) or a bias."""
+    import torch.nn as nn
+
+    E, H, S = 32, 2, 6
+    bias = torch.randn(S, S)
+
+    class Full(nn.Module):
+        def forward(self, q, k, sq, sk, bs, pos):
+            return q * 2, k, bias
+
+    class QKOnly(nn.Module):
+        def forward(self, q, k):
+            return q * 3, k * 0.5
+
+    class NoArgs(nn.Module):
+        def forward(self):
+            return bias
+
+    torch.manual_seed(0)
+    x = torch.randn(1, S, E)
+    plain = tx.FastMultiHeadAttention(E, H, kernel_type="pytorch")
+    for mod, qs, ks, b in ((Full(), 2.0, 1.0, bias), (QKOnly(), 3.0, 0.5, None), (NoArgs(), 1.0, 1.0, bias)):
+        layer = tx.FastMultiHeadAttention(E, H, kernel_type="pytorch", position_method=mod)
+        layer.load_state_dict(plain.state_dict(), strict=False)
+        q = layer.q_proj(x).view(1, S, H, -1) * qs
+        k = layer.k_proj(x).view(1, S, H, -1) * ks
+        v = layer.v_proj(x).view(1, S, H, -1)
+        w = torch.einsum("bihd,bjhd->bhij", q, k) * layer.scale
+        if b is not None:
+            w = w + b
+        ref = layer.o_proj(torch.einsum("bhij,bjhd->bihd", w.softmax(-1), v).reshape(1, S, E))
+        assert torch.allclose(layer(x), ref, atol=1e-5, rtol=1e-5), type(mod).__name__

@@ -45,7 +45,9 @@ def test_hip_layer_fp32_matches_oracle(kind, feat, kernel_type):
     if isinstance(out, tuple):
         out = out[0]
     rel = ((out.cpu() - ref).abs().max() / ref.abs().max()).item()
-    assert rel <= 1e-4, rel
+    # the north star's fp32 bar; the layer's projections run as fp32 GEMMs on
+    # the GPU and on the host (measured 0.5-1.2e-6 across these cases)
+    assert rel <= 1e-5, rel
 
 
 def test_hip_gqa_bf16_llama_block_matches_eager_and_cache():

@@ -22,7 +22,6 @@ Decisions where the reference is defective (kept in one place here):
   ``base.py:309-319,415-417``); the eager path adds the materialised bias.
 * GQA/MQA key/value heads reach the kernel un-repeated (no copy).
 """
-import warnings
 from typing import Optional, Tuple, Union
 
 import torch
@@ -189,24 +188,35 @@ class FastBaseAttention(nn.Module):
             cos, sin = self.position_embedding(q, max_seq_len)
             q, k = self.position_embedding.apply_rotary_pos_emb(q, k, cos, sin, position_ids)
         elif self.position_method == "custom" and self.position_embedding is not None:
-            try:
-                result = self.position_embedding(q, k, seq_len_q, seq_len_k, batch_size, position_ids)
-                if isinstance(result, tuple) and len(result) == 3:
-                    q, k, position_bias = result
-                elif isinstance(result, tuple) and len(result) == 2:
-                    q, k = result
-                else:
-                    position_bias = result
-            except TypeError:
-                try:
-                    result = self.position_embedding(q, k)
-                    if isinstance(result, tuple):
-                        q, k = result
-                    else:
-                        position_bias = result
-                except Exception:
-                    position_bias = self.position_embedding()
+            q, k, position_bias = self._custom_position(q, k, seq_len_q, seq_len_k, batch_size, position_ids)
         return q, k, position_bias
+
+    def _custom_position(self, q, k, seq_len_q, seq_len_k, batch_size, position_ids):
+        """A user position module, called with the calling convention user
+        modules are written against (reference base.py:239-285): the full
+        argument list first; if that signature does not fit (TypeError), just
+        (q, k); if that fails as well, no arguments (a module that returns a
+        precomputed bias).  With the full list a 3-tuple is (q, k, bias) and
+        a 2-tuple (q, k); with (q, k) any tuple is (q, k); any other result is
+        the additive bias."""
+        emb = self.position_embedding
+        full_args = (q, k, seq_len_q, seq_len_k, batch_size, position_ids)
+        try:
+            out = emb(*full_args)
+        except TypeError:
+            out = None
+        else:
+            if isinstance(out, tuple) and len(out) in (2, 3):
+                return (*out, None) if len(out) == 2 else out
+            return q, k, out
+        try:
+            out = emb(q, k)
+        except Exception:
+            return q, k, emb()
+        if isinstance(out, tuple):
+            q2, k2 = out
+            return q2, k2, None
+        return q, k, out
 
     def _alibi_slopes(self) -> Optional[torch.Tensor]:
         if self.position_method == "alibi" and self.position_embedding is not None:
@@ -248,8 +258,9 @@ class FastBaseAttention(nn.Module):
         qh = q.transpose(1, 2).contiguous().view(batch_size * num_heads, seq_len, head_dim)
         kh = k.transpose(1, 2).contiguous().view(batch_size * num_heads, seq_len_k, head_dim)
         vh = v.transpose(1, 2).contiguous().view(batch_size * num_heads, seq_len_k, head_dim)
-        # k^T materialised: bf16 bmm with a transposed-view right operand is
-        # avoided on ROCm (it has faulted the GPU); the products are the same.
+        # k^T materialised: ROCm's batched bf16 GEMM with a transposed-view
+        # right operand is a known GPU fault on this platform, so the eager
+        # path only multiplies by a contiguous k^T; the products are the same.
         w = torch.bmm(qh, kh.transpose(-2, -1).contiguous()) * self.scale
         if self.causal:
             w.masked_fill_(torch.triu(torch.ones(seq_len, seq_len_k, device=q.device), diagonal=1).bool(),
