@@ -37,6 +37,12 @@
  *                                 RoPE in the layers: base.py:163-176,
  *                                 grouped_query_attention.py:171-177,
  *                                 trinix/layers/norm/rmsnorm.py:62-75
+ *   trinix_qk_layernorm        <- the same with qk_norm_type='layernorm' (FastLayerNorm
+ *                                 over head_dim): base.py:167-169,
+ *                                 trinix/layers/norm/layernorm.py:83-88
+ *   trinix_qk_norm_bwd         <- the autograd backward of those eager modules and of
+ *                                 the RoPE before them (rope.py:111-118), which the
+ *                                 reference's layers train through
  *   trinix_alibi_bias          <- TritonALiBiKernel.apply / FastALiBiPositionEmbedding
  *                                 trinix/kernels/alibi_kernel.py:8-54,93-124,
  *                                 trinix/layers/embeddings/alibi.py:65-90
@@ -54,7 +60,7 @@
 extern "C" {
 #endif
 
-#define TRINIX_ATTN_ABI_VERSION 3
+#define TRINIX_ATTN_ABI_VERSION 4
 
 typedef enum trinix_status {
   TRINIX_OK = 0,
@@ -222,6 +228,49 @@ int trinix_qk_norm(const void* x, const int64_t x_stride[4], void* out,
                    const void* weight, float eps, const void* cos,
                    const void* sin, int64_t cs_stride, int64_t cs_rows,
                    const int64_t* position_ids, void* stream);
+
+/* LayerNorm variant of trinix_qk_norm (reference qk_norm_type='layernorm',
+ * trinix/layers/attention/base.py:167-169: FastLayerNorm's PyTorch path
+ * trinix/layers/norm/layernorm.py:83-88, F.layer_norm with weight and bias
+ * cast to the input dtype):
+ *   y   = cos ? rope(x) : x
+ *   out = to_dtype((y - mean_d(y)) * rsqrt(var_d(y) + eps) * weight + bias)
+ * in fp32 (biased variance); weight and bias of head_dim elements in the
+ * dtype of x.  Other arguments as for trinix_qk_norm.  ABI version 4. */
+int trinix_qk_layernorm(const void* x, const int64_t x_stride[4], void* out,
+                        const int64_t out_stride[4], int64_t batch,
+                        int64_t seqlen, int64_t nheads, int64_t head_dim,
+                        int32_t dtype, const void* weight, const void* bias,
+                        float eps, const void* cos, const void* sin,
+                        int64_t cs_stride, int64_t cs_rows,
+                        const int64_t* position_ids, void* stream);
+
+/* norm_type of trinix_qk_norm_bwd */
+#define TRINIX_NORM_RMS 0   /* trinix_qk_norm */
+#define TRINIX_NORM_LAYER 1 /* trinix_qk_layernorm */
+
+/* Backward of trinix_qk_norm / trinix_qk_layernorm: the gradients eager
+ * autograd gives through the RoPE and the norm modules the reference's
+ * layers train with (base.py:163-176, rmsnorm.py:62-75, layernorm.py:83-88,
+ * rope.py:111-118).  x is the forward's input (before RoPE), dout the
+ * gradient of its output; dx (same layout rules as x) receives the gradient
+ * of x.  dweight_partial (and, for TRINIX_NORM_LAYER, dbias_partial) are
+ * caller-provided fp32 arrays of partial_rows x head_dim elements: row r
+ * receives the column sums of workgroup r (partial_rows workgroups walk the
+ * rows; any partial_rows >= 1 is valid).  The caller adds the rows and
+ * rounds to the weight's dtype to get dweight (dbias).  eps, weight, cos,
+ * sin, cs_stride, cs_rows and position_ids are the forward's.  ABI
+ * version 4. */
+int trinix_qk_norm_bwd(const void* x, const int64_t x_stride[4],
+                       const void* dout, const int64_t dout_stride[4],
+                       void* dx, const int64_t dx_stride[4], int64_t batch,
+                       int64_t seqlen, int64_t nheads, int64_t head_dim,
+                       int32_t dtype, int32_t norm_type, const void* weight,
+                       float eps, const void* cos, const void* sin,
+                       int64_t cs_stride, int64_t cs_rows,
+                       const int64_t* position_ids, float* dweight_partial,
+                       float* dbias_partial, int64_t partial_rows,
+                       void* stream);
 
 /* Backward of trinix_attn_fwd.  No counterpart in the reference (its
  * Triton attention has no backward, attention_kernel.py:497-517); the

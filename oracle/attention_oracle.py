@@ -29,6 +29,12 @@ path the north star names as the parity target, the eager
   layers build at base.py:163-176 and apply after RoPE
   (grouped_query_attention.py:171-177); head_dim <= 2048 always takes this
   path in the reference.
+* ``qk_layer_norm``    <- ``FastLayerNorm._pytorch_forward``
+  (trinix/layers/norm/layernorm.py:83-88), the qk-norm of
+  ``qk_norm_type='layernorm'`` (base.py:167-169): ``F.layer_norm`` with the
+  weight and bias cast to the input dtype; head_dim <= 4096 always takes this
+  path.  Both norms are differentiable torch ops: their autograd is the
+  reference's backward.
 * ``functional_attention`` composes them the way the layers feed the eager
   path: window mask + user mask + ALiBi bias summed in fp32
   (base.py:309-319) and added into the q.dtype scores (base.py:392).
@@ -57,6 +63,7 @@ __all__ = [
     "tile_kv_heads",
     "rope_tables",
     "apply_rope",
+    "qk_layer_norm",
     "alibi_slopes",
     "alibi_bias",
     "window_bias",
@@ -150,6 +157,12 @@ def qk_rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
     h = x.to(torch.float32)
     h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
     return weight * h.to(dt)
+
+
+def qk_layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float) -> torch.Tensor:
+    """F.layer_norm over the last dim with weight and bias cast to x.dtype
+    (layernorm.py:83-88)."""
+    return F.layer_norm(x, (x.shape[-1],), weight.to(x.dtype), bias.to(x.dtype), eps)
 
 
 def alibi_slopes(num_heads: int) -> torch.Tensor:

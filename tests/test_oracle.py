@@ -266,6 +266,39 @@ def test_qk_rms_norm_pinned():
     assert (yb.float() - y).abs().max() <= 2 ** -6 * y.abs().max()
 
 
+def test_qk_layer_norm_pinned():
+    """The qk LayerNorm restatement against an fp64 per-row loop (biased
+    variance), its bf16 evaluation within the rounding of its fp32 one, and
+    the gradients of its autograd (the reference's backward) against an
+    fp64 finite difference."""
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(2, 3, 4, 32, generator=g)
+    w, b = torch.randn(32, generator=g), torch.randn(32, generator=g)
+    y = orc.qk_layer_norm(x, w, b, 1e-5)
+    xd, wd, bd = x.double().numpy(), w.double().numpy(), b.double().numpy()
+    for idx in np.ndindex(2, 3, 4):
+        row = xd[idx]
+        mu = sum(row) / 32
+        var = sum((v - mu) ** 2 for v in row) / 32
+        want = (row - mu) / math.sqrt(var + 1e-5) * wd + bd
+        assert np.allclose(y[idx].double().numpy(), want, rtol=1e-5, atol=1e-5)
+    yb = orc.qk_layer_norm(x.bfloat16(), w, b, 1e-5)
+    assert yb.dtype == torch.bfloat16
+    assert (yb.float() - y).abs().max() <= 2 ** -6 * y.abs().max() + 2 ** -6
+    # d/dx of sum(c * y) by central differences in fp64
+    xx = x[0, 0, :1].double().requires_grad_(True)
+    c = torch.randn(1, 32, generator=g).double()
+    (orc.qk_layer_norm(xx, w.double(), b.double(), 1e-5) * c).sum().backward()
+    h = 1e-6
+    for j in (0, 7, 31):
+        e = torch.zeros_like(xx)
+        e[0, j] = h
+        with torch.no_grad():
+            fd = ((orc.qk_layer_norm(xx + e, w.double(), b.double(), 1e-5) * c).sum()
+                  - (orc.qk_layer_norm(xx - e, w.double(), b.double(), 1e-5) * c).sum()) / (2 * h)
+        assert abs(fd.item() - xx.grad[0, j].item()) <= 1e-6 * max(1.0, abs(fd.item()))
+
+
 def test_row_and_key_bands_equal_full_evaluation():
     """A row band (and a key range covering the band) gives the rows of the
     full evaluation: causal, window, ALiBi and a user mask at absolute

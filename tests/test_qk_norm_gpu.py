@@ -1,19 +1,33 @@
-"""GPU tests of the fused qk-norm (``trinix_qk_norm``: RoPE + RMSNorm over
-head_dim) against the oracle's restatement of the reference's eager path
-(``orc.apply_rope`` then ``orc.qk_rms_norm``, trinix/layers/norm/rmsnorm.py:
-62-75), and of the layers that use it.
+"""GPU tests of the fused qk-norm (``trinix_qk_norm`` / ``trinix_qk_layernorm``:
+RoPE + RMSNorm or LayerNorm over head_dim, and ``trinix_qk_norm_bwd``)
+against the oracle's restatement of the reference's eager path
+(``orc.apply_rope`` then ``orc.qk_rms_norm`` / ``orc.qk_layer_norm``,
+trinix/layers/norm/rmsnorm.py:62-75, layernorm.py:83-88), its autograd on the
+CPU for the backward, and of the layers that use them.
 
-Bar: the fp32 sum of squares is ordered differently from torch's reduction,
-so the normalisation factor can differ by an ulp of fp32 and an output
-element by an ulp or two of the dtype.  At least 99% of the elements must be
+Bar: the fp32 reductions are ordered differently from torch's, so a
+normalisation factor can differ by an ulp of fp32 and an output element by
+an ulp or two of the dtype.  Forward: at least 99% of the elements
 bit-identical to the oracle and every element within 2 ulps of it.
+Backward, RMSNorm: the gradient is a difference of two terms (the direct
+one and the one through the row statistics), which cancel near zero; there
+an fp32 rounding difference is large relative to the element, so the bar
+adds 1e-3 of the tensor's largest element to the 2 ulps, and 98%
+bit-identical.  dweight sums the rows in fp32 in another order: 2 ulps of
+the dtype plus 1e-3 of the largest element.
+Backward, LayerNorm: torch's CPU layer_norm backward rounds its
+intermediate products differently from the fp32 formula (dx is about 70%
+bit-identical, within an ulp or two), and the reference's path is torch's
+GPU kernel anyway; so the bar is the one of the attention backward: the
+error against the fp64 gradient at most twice the eager bf16/fp16 error plus
+1e-3 of the largest element.
 """
 import pytest
 import torch
 
 from oracle import attention_oracle as orc
 import trinix_amd as tx
-from trinix_amd.kernels import qk_rmsnorm
+from trinix_amd.kernels import qk_layernorm, qk_rmsnorm
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -95,18 +109,155 @@ def test_gqa_layer_with_qk_norm_uses_fused_kernel_in_inference():
     assert d.max().item() <= 2e-2 * scale and d.mean().item() <= 2e-3 * scale, d.max().item()
 
 
-def test_qk_norm_layer_training_keeps_eager_gradients():
-    torch.manual_seed(13)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [16, 64, 128, 256])
+@pytest.mark.parametrize("rope", [False, True])
+def test_qk_layernorm_matches_oracle(D, dtype, rope):
+    g = torch.Generator().manual_seed(100 + D + (1 if rope else 0))
+    B, S, H = 2, 37, 5
+    x = (3 * torch.randn(B, S, H, D, generator=g) + 0.5).to(dtype)
+    w = (1 + 0.3 * torch.randn(D, generator=g)).to(dtype)
+    b = (0.2 * torch.randn(D, generator=g)).to(dtype)
+    cos = sin = None
+    xr = x
+    if rope:
+        cos, sin = orc.rope_tables(S, D, 10000.0, dtype)
+        xr = orc.apply_rope(x, cos, sin)
+    ref = orc.qk_layer_norm(xr, w, b, 1e-5)
+    out = qk_layernorm(x.to(DEV), w.to(DEV), b.to(DEV), 1e-5, None if cos is None else cos.to(DEV),
+                       None if sin is None else sin.to(DEV))
+    assert_ulps(out, ref, f"layernorm D={D} {dtype} rope={rope}")
+
+
+def assert_grad(out, ref, what, frac=0.98):
+    out, ref = out.detach().cpu(), ref.detach().cpu()
+    assert out.dtype == ref.dtype and out.shape == ref.shape, what
+    d = (out.float() - ref.float()).abs()
+    bar = 2 * ulp(ref) + 1e-3 * ref.float().abs().max()
+    same = (out == ref).float().mean().item()
+    assert (d <= bar).all(), f"{what}: max diff {d.max().item():.3g} (largest element {ref.float().abs().max():.3g})"
+    assert same >= frac, f"{what}: only {same:.4f} bit-identical"
+
+
+def _norm_case(norm, D, dtype, rope, positions, seed):
+    g = torch.Generator().manual_seed(seed)
+    B, S, H = 2, 45, 3
+    x = (2 * torch.randn(B, S, H, D, generator=g) + 0.3).to(dtype)
+    w = (1 + 0.3 * torch.randn(D, generator=g)).to(dtype)
+    b = (0.2 * torch.randn(D, generator=g)).to(dtype) if norm == "layer" else None
+    dout = torch.randn(B, S, H, D, generator=g).to(dtype)
+    cos = sin = pos = None
+    if rope:
+        cos, sin = orc.rope_tables(64, D, 10000.0, dtype)
+        if positions:
+            pos = torch.randint(0, 64, (B, S), generator=g)
+    return x, w, b, dout, cos, sin, pos
+
+
+@pytest.mark.parametrize("norm", ["rms", "layer"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+@pytest.mark.parametrize("rope", ["none", "rope", "rope+positions"])
+def test_qk_norm_backward_matches_eager_autograd(norm, dtype, D, rope):
+    """dx, dweight (and dbias) of the fused kernels against autograd through
+    the oracle's eager RoPE and norm on the CPU (the reference's backward)."""
+    x, w, b, dout, cos, sin, pos = _norm_case(norm, D, dtype, rope != "none", rope == "rope+positions",
+                                              seed=D + 7 * len(rope) + (1 if norm == "layer" else 0))
+    eps = 1e-6 if norm == "rms" else 1e-5
+
+    def eager(dt):
+        leaves = [t.detach().to(dt).clone().requires_grad_(True) for t in (x, w) + ((b,) if b is not None else ())]
+        c, s_ = (None, None) if cos is None else (cos.to(dt), sin.to(dt))
+        xr = orc.apply_rope(leaves[0], c, s_, pos) if c is not None else leaves[0]
+        y = orc.qk_rms_norm(xr, leaves[1], eps) if norm == "rms" else orc.qk_layer_norm(xr, leaves[1], leaves[2], eps)
+        y.backward(dout.to(dt))
+        return y, leaves
+
+    ref, leaves = eager(dtype)
+    dev = [t.detach().to(DEV).requires_grad_(True) for t in (x, w) + ((b,) if b is not None else ())]
+    tabs = [None if t is None else t.to(DEV) for t in (cos, sin, pos)]
+    if norm == "rms":
+        out = qk_rmsnorm(dev[0], dev[1], eps, *tabs)
+    else:
+        out = qk_layernorm(dev[0], dev[1], dev[2], eps, *tabs)
+    out.backward(dout.to(DEV))
+    what = f"{norm} D={D} {dtype} {rope}"
+    assert_ulps(out.detach(), ref.detach(), what + " forward")
+    if norm == "rms":
+        assert_grad(dev[0].grad, leaves[0].grad, what + " dx")
+        assert_grad(dev[1].grad, leaves[1].grad, what + " dweight", frac=0.0)
+    else:
+        _, truth = eager(torch.float64)
+        for name, h, e, t in zip(("dx", "dweight", "dbias"), dev, leaves, truth):
+            t64 = t.grad
+            err_h = (h.grad.cpu().double() - t64).abs().max().item()
+            err_e = (e.grad.double() - t64).abs().max().item()
+            scale = t64.abs().max().item()
+            assert err_h <= 2 * err_e + 1e-3 * scale, (what, name, err_h, err_e, scale)
+
+
+def test_qk_norm_backward_strided_input_and_gradient():
+    """A head-major (B, S, H, D) view as input and a non-contiguous output
+    gradient: the same gradients as contiguous copies."""
+    x, w, _, dout, cos, sin, _ = _norm_case("rms", 128, torch.bfloat16, True, False, seed=77)
+    xd = x.permute(0, 2, 1, 3).contiguous().to(DEV).permute(0, 2, 1, 3).requires_grad_(True)
+    assert not xd.is_contiguous()
+    wd = w.to(DEV).requires_grad_(True)
+    out = qk_rmsnorm(xd, wd, 1e-6, cos.to(DEV), sin.to(DEV))
+    g = dout.to(DEV).permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+    out.backward(g)
+    xc = x.to(DEV).requires_grad_(True)
+    wc = w.to(DEV).requires_grad_(True)
+    qk_rmsnorm(xc, wc, 1e-6, cos.to(DEV), sin.to(DEV)).backward(dout.to(DEV))
+    assert torch.equal(xd.grad, xc.grad) and torch.equal(wd.grad, wc.grad)
+
+
+@pytest.mark.parametrize("norm_type", ["rmsnorm", "layernorm"])
+def test_qk_norm_layer_training_uses_fused_kernels(norm_type, monkeypatch):
+    """A GQA layer training step with qk_norm: the fused kernels (forward and
+    backward) replace the eager norm modules, and the gradients of x, the
+    projections and the norm parameters are within twice the bf16 eager
+    layer's error (against fp64) plus 2e-3 of the largest element."""
+    from trinix_amd.layers.attention import base as lb
+
+    torch.manual_seed(13 + len(norm_type))
     E, H, HKV, S = 512, 4, 2, 64
-    layer = tx.FastGroupedQueryAttention(E, H, HKV, kernel_type="flash", position_method="rope", qk_norm=True,
-                                         causal=True).to(DEV, torch.bfloat16)
-    x = torch.randn(1, S, E, device=DEV).to(torch.bfloat16).requires_grad_(True)
-    q = torch.empty(1, 1, H, E // H, device=DEV, dtype=torch.bfloat16, requires_grad=True)
-    assert not layer._fused_qk_norm_applies(q, q)
-    out, _ = layer(x)
-    out.float().sum().backward()
-    assert layer.q_norm.weight.grad is not None and layer.k_norm.weight.grad is not None
-    assert torch.isfinite(x.grad).all()
+    kw = dict(causal=True, position_method="rope", rope_base=10000.0, qk_norm=True, qk_norm_type=norm_type)
+    hip = tx.FastGroupedQueryAttention(E, H, HKV, kernel_type="flash", **kw)
+    with torch.no_grad():
+        hip.q_norm.weight.uniform_(0.5, 1.5)
+        hip.k_norm.weight.uniform_(0.5, 1.5)
+        if norm_type == "layernorm":
+            hip.q_norm.bias.uniform_(-0.2, 0.2)
+            hip.k_norm.bias.uniform_(-0.2, 0.2)
+    ref64 = tx.FastGroupedQueryAttention(E, H, HKV, kernel_type="pytorch", **kw).double()
+    ref16 = tx.FastGroupedQueryAttention(E, H, HKV, kernel_type="pytorch", **kw).to(torch.bfloat16)
+    ref64.load_state_dict(hip.state_dict())
+    ref16.load_state_dict(hip.state_dict())
+    hip = hip.to(DEV, torch.bfloat16)
+    names = ["q_proj.weight", "k_proj.weight", "v_proj.weight", "q_norm.weight", "k_norm.weight"]
+    if norm_type == "layernorm":
+        names += ["q_norm.bias", "k_norm.bias"]
+    x = torch.randn(2, S, E)
+    gy = torch.randn(2, S, E)
+    grads, outs = [], []
+    for layer, dev, dt in ((ref64, "cpu", torch.float64), (ref16, "cpu", torch.bfloat16), (hip, DEV, torch.bfloat16)):
+        if layer is hip:  # the eager norm modules must not run on the fused path
+            def refuse(self, x):
+                raise AssertionError("eager qk-norm module called")
+            monkeypatch.setattr(lb._QKRMSNorm, "forward", refuse)
+            monkeypatch.setattr(lb._QKLayerNorm, "forward", refuse)
+        xi = x.to(dev, dt).requires_grad_(True)
+        y, _ = layer(xi)
+        y.backward(gy.to(dev, dt))
+        outs.append(y.detach().cpu().double())
+        grads.append([xi.grad.cpu().double()] + [layer.get_parameter(n).grad.cpu().double() for n in names])
+    t, e, h = grads
+    assert (outs[2] - outs[0]).abs().max() <= 2 * (outs[1] - outs[0]).abs().max() + 2e-3 * outs[0].abs().max()
+    for name, gh, gt, ge in zip(["x"] + names, h, t, e):
+        scale = gt.abs().max().item()
+        err_h, err_e = (gh - gt).abs().max().item(), (ge - gt).abs().max().item()
+        assert err_h <= 2 * err_e + 2e-3 * scale, (name, err_h, err_e, scale)
 
 
 def _rope_tables(q, S):

@@ -37,7 +37,7 @@ TRINIX_U8 = 3
 BLOCKMAP_ROWS = 32
 BLOCKMAP_COLS = 64
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 Int64x4 = c_int64 * 4
 Int64x2 = c_int64 * 2
@@ -165,6 +165,17 @@ SIGNATURES = {
         c_int32,
         [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64, c_int32,
          c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p],
+    ),
+    "trinix_qk_layernorm": (
+        c_int32,
+        [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64, c_int64, c_int64, c_int32,
+         c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p],
+    ),
+    "trinix_qk_norm_bwd": (
+        c_int32,
+        [c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_void_p, POINTER(c_int64), c_int64, c_int64,
+         c_int64, c_int64, c_int32, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+         c_void_p, c_void_p, c_int64, c_void_p],
     ),
     "trinix_alibi_bias": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "trinix_attn_tile_config": (c_int32, [c_int64, c_int32, POINTER(TileCfg)]),

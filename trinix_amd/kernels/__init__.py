@@ -2,7 +2,7 @@
 ``trinix/kernels/__init__.py:14`` for drop-in use."""
 from .alibi_kernel import TritonALiBiKernel, alibi_bias
 from .attention_kernel import TritonAttentionKernel, attention_flops, allowed_pairs
-from .qk_norm_kernel import qk_norm_supported, qk_rmsnorm
+from .qk_norm_kernel import qk_layernorm, qk_norm_supported, qk_rmsnorm
 from .rope_kernel import TritonRoPEKernel, rope_apply
 from .utils import calculate_attention_block_sizes, get_cuda_compute_capability, tile_config
 
@@ -13,6 +13,7 @@ __all__ = [
     "TritonRoPEKernel",
     "rope_apply",
     "qk_rmsnorm",
+    "qk_layernorm",
     "qk_norm_supported",
     "attention_flops",
     "allowed_pairs",

@@ -308,20 +308,32 @@ class FastBaseAttention(nn.Module):
         return self._apply_pytorch_attention(q, k, v, attn_mask)
 
     def _fused_qk_norm_applies(self, q, k) -> bool:
-        """qk RMSNorm (+ RoPE) through the fused kernel: GPU kernel path,
-        RMSNorm weights in the activations' 16-bit dtype, a supported
-        head_dim, RoPE / ALiBi / no position encoding, and no gradient needed
-        (the fused kernel has no backward; training keeps the eager modules)."""
-        if not (self.qk_norm and isinstance(self.q_norm, _QKRMSNorm) and self._uses_kernel(q)):
+        """qk-norm (+ RoPE) through the fused kernels (differentiable): GPU
+        kernel path, a supported head_dim, RoPE / ALiBi / no position
+        encoding; RMSNorm weights in the activations' 16-bit dtype (the eager
+        module's output is then that dtype), LayerNorm weights of any float
+        dtype (the eager module casts them to the activations' dtype)."""
+        if not (self.qk_norm and self._uses_kernel(q)):
             return False
         if self.position_method not in ("rope", "alibi", "none"):
             return False
-        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or self.q_norm.weight.requires_grad
-                                        or self.k_norm.weight.requires_grad):
-            return False
         from ...kernels.qk_norm_kernel import qk_norm_supported
 
-        return qk_norm_supported(q, self.q_norm.weight) and qk_norm_supported(k, self.k_norm.weight)
+        if isinstance(self.q_norm, _QKRMSNorm):
+            return qk_norm_supported(q, self.q_norm.weight) and qk_norm_supported(k, self.k_norm.weight)
+        if isinstance(self.q_norm, _QKLayerNorm):
+            return (qk_norm_supported(q, self.q_norm.weight.detach().to(q.dtype))
+                    and qk_norm_supported(k, self.k_norm.weight.detach().to(k.dtype)))
+        return False
+
+    def _fused_qk_norm(self, norm, x, cos, sin, position_ids):
+        """The layer's q_norm / k_norm module applied (after RoPE when
+        cos/sin are given) by the fused kernel."""
+        from ...kernels.qk_norm_kernel import qk_layernorm, qk_rmsnorm
+
+        if isinstance(norm, _QKLayerNorm):
+            return qk_layernorm(x, norm.weight.to(x.dtype), norm.bias.to(x.dtype), norm.eps, cos, sin, position_ids)
+        return qk_rmsnorm(x, norm.weight, norm.eps, cos, sin, position_ids)
 
     # -- shared layer body ------------------------------------------------------
     def _attend(self, q, k, v, attention_mask, position_ids, past_key_value, use_zero_attn):
@@ -336,10 +348,13 @@ class FastBaseAttention(nn.Module):
         fuse_norm = self._fused_qk_norm_applies(q, k)
         # q's RoPE + RMSNorm in the attention kernel's prologue (positions are
         # the query rows: no position_ids, no cache, no zero-attention row;
-        # that kernel takes no mask and no dropout)
-        fuse_qnorm = (self.fuse_q_norm_in_attention and fuse_norm and position_ids is None and past_key_value is None
+        # that kernel takes no mask and no dropout, and has no backward
+        # through the norm)
+        fuse_qnorm = (self.fuse_q_norm_in_attention and fuse_norm and isinstance(self.q_norm, _QKRMSNorm)
+                      and position_ids is None and past_key_value is None
                       and not (use_zero_attn and self.add_zero_attn) and q.shape[-1] in (64, 128, 256)
-                      and attention_mask is None and not (self.training and self.dropout > 0.0))
+                      and attention_mask is None and not (self.training and self.dropout > 0.0)
+                      and not (torch.is_grad_enabled() and (q.requires_grad or self.q_norm.weight.requires_grad)))
         if fuse_rope:
             # q is rotated inside the attention kernel; k by the RoPE kernel
             # (it is also the returned cache).
@@ -349,18 +364,16 @@ class FastBaseAttention(nn.Module):
             k = rotate(k, cos, sin)
             rotary = (cos, sin)
         elif fuse_norm:
-            # RoPE (if any) and the qk RMSNorm in one kernel pass per tensor
+            # RoPE (if any) and the qk-norm in one kernel pass per tensor
             # (the eager order: rotate, then normalise).
-            from ...kernels.qk_norm_kernel import qk_rmsnorm
-
             cos = sin = None
             if self.position_method == "rope" and self.position_embedding is not None:
                 cos, sin = self.position_embedding(q, max(seq_len_q, seq_len_k))
             if fuse_qnorm:
                 rotary = (cos, sin) if cos is not None else None
             else:
-                q = qk_rmsnorm(q, self.q_norm.weight, self.q_norm.eps, cos, sin, position_ids)
-            k = qk_rmsnorm(k, self.k_norm.weight, self.k_norm.eps, cos, sin, position_ids)
+                q = self._fused_qk_norm(self.q_norm, q, cos, sin, position_ids)
+            k = self._fused_qk_norm(self.k_norm, k, cos, sin, position_ids)
             attention_mask = self._merge_position_bias(attention_mask, None)
         else:
             q, k, position_bias = self._apply_position_embedding(q, k, seq_len_q, seq_len_k, bs, position_ids)
