@@ -243,6 +243,40 @@ def test_qk_norm_rejects_before_launch(lib):
                                  None, None) == nat.TRINIX_ERR_BAD_SHAPE
 
 
+def test_qk_layernorm_and_backward_reject_before_launch(lib):
+    st = (ctypes.c_int64 * 4)(8 * 64 * 128, 8 * 128, 128, 1)
+
+    def ln(x=4096, w=4096, b=4096, D=128, dtype=nat.TRINIX_BF16):
+        return lib.trinix_qk_layernorm(x, st, 4096, st, 1, 64, 8, D, dtype, w, b, 1e-5, None, None, 0, 0, None,
+                                       None)
+
+    assert ln(b=None) == nat.TRINIX_ERR_NULL_POINTER  # LayerNorm needs its bias
+    assert ln(D=48) == nat.TRINIX_ERR_BAD_HEAD_DIM
+    assert ln(dtype=nat.TRINIX_F32) == nat.TRINIX_ERR_BAD_DTYPE
+    assert ln(b=4100) == nat.TRINIX_ERR_BAD_STRIDE
+
+    def bwd(norm=nat.TRINIX_NORM_RMS, dwp=4096, dbp=None, rows=16, dx=4096, dout=4096, cos=None):
+        return lib.trinix_qk_norm_bwd(4096, st, dout, st, dx, st, 1, 64, 8, 128, nat.TRINIX_BF16, norm, 4096, 1e-6,
+                                      cos, None, 64, 64, None, dwp, dbp, rows, None)
+
+    assert bwd(norm=7) == nat.TRINIX_ERR_BAD_ARGUMENT
+    assert bwd(dwp=None) == nat.TRINIX_ERR_NULL_POINTER
+    assert bwd(norm=nat.TRINIX_NORM_LAYER) == nat.TRINIX_ERR_NULL_POINTER  # no dbias partials
+    assert bwd(rows=0) == nat.TRINIX_ERR_BAD_SHAPE
+    assert bwd(dx=None) == nat.TRINIX_ERR_NULL_POINTER
+    assert bwd(dout=4104) == nat.TRINIX_ERR_BAD_STRIDE
+    assert bwd(cos=4096) == nat.TRINIX_ERR_NULL_POINTER  # cos without sin
+
+
+def test_qk_norm_backward_partial_rows():
+    from trinix_amd.kernels.qk_norm_kernel import partial_rows
+
+    assert partial_rows(1, 128) == 1
+    assert partial_rows(32, 128) == 1 and partial_rows(33, 128) == 2  # 32 rows per pass at D = 128
+    assert partial_rows(10 ** 7, 64) == 1024
+    assert partial_rows(16, 16) == 1  # 256 rows per pass at D = 16
+
+
 def test_splitkv_plan_invariants_random(lib):
     """For random decode shapes the plan's chunks tile the visible keys:
     chunk a multiple of 64 and >= 64, ceil(span / chunk) chunks, workspace =

@@ -34,6 +34,9 @@ TRINIX_F16 = 1
 TRINIX_BF16 = 2
 TRINIX_U8 = 3
 
+TRINIX_NORM_RMS = 0
+TRINIX_NORM_LAYER = 1
+
 BLOCKMAP_ROWS = 32
 BLOCKMAP_COLS = 64
 

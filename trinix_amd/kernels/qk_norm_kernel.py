@@ -28,7 +28,7 @@ from .attention_kernel import _DTYPE_CODE, current_stream_ptr
 from .rope_kernel import _table, check_positions
 
 QK_NORM_HEAD_DIMS = (16, 32, 64, 128, 256)
-NORM_RMS, NORM_LAYER = 0, 1  # TRINIX_NORM_RMS / TRINIX_NORM_LAYER
+NORM_RMS, NORM_LAYER = nat.TRINIX_NORM_RMS, nat.TRINIX_NORM_LAYER
 # at most this many workgroups (rows of dweight partial sums) in a backward
 _MAX_PARTIAL_ROWS = 1024
 
