@@ -269,10 +269,12 @@ def _rope_tables(q, S):
 @pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("rope", [False, True])
 @pytest.mark.parametrize("Sq", [150, 8])
-def test_q_norm_fused_into_attention_is_bitwise_the_two_kernel_path(D, dtype, rope, Sq, monkeypatch):
+@pytest.mark.parametrize("alibi", [False, True])
+def test_q_norm_fused_into_attention_is_bitwise_the_two_kernel_path(D, dtype, rope, Sq, alibi, monkeypatch):
     """q's RoPE + RMSNorm in the attention kernel's prologue gives the
     output of qk_rmsnorm followed by the attention kernel, bit for bit (the
-    prologue repeats qk_rmsnorm's rounding and its sum-of-squares order)."""
+    prologue repeats qk_rmsnorm's rounding and its sum-of-squares order),
+    with and without ALiBi (both are built with the fused norm)."""
     from trinix_amd.kernels import TritonAttentionKernel, rope_apply
     from trinix_amd.kernels import attention_kernel as ak
 
@@ -292,7 +294,10 @@ def test_q_norm_fused_into_attention_is_bitwise_the_two_kernel_path(D, dtype, ro
         cos, sin = _rope_tables(q, max(Sq, Sk))
         k = rope_apply(k, cos, sin)
         kw = dict(rotary_cos=cos, rotary_sin=sin, rotary_k=False)
-    ref = TritonAttentionKernel.apply(qk_rmsnorm(q, w, eps, cos, sin), k, v, causal=True)
+    if alibi:
+        kw["alibi_slopes"] = orc.alibi_slopes(H).to(DEV, torch.float32)
+    ref = TritonAttentionKernel.apply(qk_rmsnorm(q, w, eps, cos, sin), k, v, causal=True,
+                                      alibi_slopes=kw.get("alibi_slopes"))
     out = TritonAttentionKernel.apply(q, k, v, causal=True, q_norm_weight=w, q_norm_eps=eps, **kw)
     assert torch.equal(out, ref)
 
