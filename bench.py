@@ -279,8 +279,10 @@ def layer_measure(torch, iters=10):
     three ways: q's RoPE + RMSNorm in the attention prologue and k's in the
     fused RoPE + qk RMSNorm kernel (the default); both through that kernel;
     the eager norm modules.  Plus that kernel alone on q (algorithmic bytes:
-    q read and written once).  The projections are torch Linear layers
-    (hipBLASLt GEMMs)."""
+    q read and written once) and its backward on q (x and dout read, dx
+    written), and a training step (forward + backward) of the layer with
+    the fused and with the eager qk-norm.  The projections are torch Linear
+    layers (hipBLASLt GEMMs)."""
     import trinix_amd as tx
     from trinix_amd.kernels import qk_rmsnorm
 
@@ -309,6 +311,36 @@ def layer_measure(torch, iters=10):
                 us = time_events(lambda: qk_rmsnorm(q, w, 1e-6, cos, sin), 20, torch) * 1e3
             res["qk_norm_kernel_q_us"] = round(us, 2)
             res["qk_norm_kernel_q_gbps"] = round(2 * q.numel() * 2 / (us * 1e-6) / 1e9, 1)
+            # its backward on q (dx, and dweight from the per-workgroup
+            # partial rows): x and dout read, dx written once
+            from trinix_amd.kernels.qk_norm_kernel import NORM_RMS, _backward, _tables
+
+            dout = torch.randn_like(q)
+            c, s_, _ = _tables(q, cos, sin, None)
+            _backward(q, dout, w, 1e-6, c, s_, None, NORM_RMS)
+            us = time_events(lambda: _backward(q, dout, w, 1e-6, c, s_, None, NORM_RMS), 20, torch) * 1e3
+            res["qk_norm_bwd_q_us"] = round(us, 2)
+            res["qk_norm_bwd_q_gbps"] = round(3 * q.numel() * 2 / (us * 1e-6) / 1e9, 1)
+        del layer
+    # a training step of the layer (forward + backward to x and the
+    # parameters): qk-norm through the fused kernels against the eager modules
+    for mode in ("us_train_step_fused_qk_norm", "us_train_step_eager_qk_norm"):
+        layer = tx.FastGroupedQueryAttention(H * D, H, HKV, causal=True, position_method="rope", rope_base=500000.0,
+                                             qk_norm=True, max_seq_len=S).to("cuda", torch.bfloat16)
+        if mode == "us_train_step_eager_qk_norm":
+            layer._fused_qk_norm_applies = lambda q, k: False
+        xg = x.detach().clone().requires_grad_(True)
+        gy = torch.randn_like(x)
+
+        def step():
+            xg.grad = None
+            for prm in layer.parameters():
+                prm.grad = None
+            layer(xg)[0].backward(gy)
+
+        for _ in range(2):
+            step()
+        res[mode] = round(time_events(step, 5, torch) * 1e3, 1)
         del layer
     return res
 

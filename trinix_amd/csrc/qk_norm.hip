@@ -169,8 +169,10 @@ __global__ __launch_bounds__(256) void qk_norm_kernel(const uint16_t* x, int64_t
 // Backward.  Each workgroup walks rows blockIdx.x*RPB + k*gridDim.x*RPB
 // (RPB = 256/NCH rows per pass) and writes its fp32 dweight (and, for
 // LayerNorm, dbias) column sums to row blockIdx.x of the partial arrays.
+// RMSNorm fits four wavefronts per SIMD (128 registers); LayerNorm, with
+// its dbias sums, three.
 template <class E, bool LN>
-__global__ __launch_bounds__(256) void qk_norm_bwd_kernel(
+__global__ __launch_bounds__(256, LN ? 3 : 4) void qk_norm_bwd_kernel(
     const uint16_t* x, int64_t xsb, int64_t xss, int64_t xsh, const uint16_t* dout, int64_t gsb, int64_t gss,
     int64_t gsh, uint16_t* dx, int64_t osb, int64_t oss, int64_t osh, int S, int H, int D, const uint16_t* w,
     float eps, const uint16_t* cosp, const uint16_t* sinp, int64_t cs, int64_t cs_rows, const int64_t* pos,
@@ -182,11 +184,13 @@ __global__ __launch_bounds__(256) void qk_norm_bwd_kernel(
   const int rpb = 256 / nch;
   const int lrow = threadIdx.x / nch, c = threadIdx.x % nch;
   const int d = c * 8, half = D / 2;
-  float w1[8], w2[8];
-  unpack8<E>(*(const u32x4_t*)(w + d), w1);
-  unpack8<E>(*(const u32x4_t*)(w + d + half), w2);
   float aw[16] = {}, ab[16] = {};
   for (int64_t row0 = (int64_t)blockIdx.x * rpb; row0 < rows; row0 += (int64_t)gridDim.x * rpb) {
+    // the weight is read per row (cache-resident) rather than held across
+    // the loop: registers for four wavefronts per SIMD
+    float w1[8], w2[8];
+    unpack8<E>(*(const u32x4_t*)(w + d), w1);
+    unpack8<E>(*(const u32x4_t*)(w + d + half), w2);
     const int64_t row_t = row0 + lrow;
     const bool live = row_t < rows;
     const RowPos rp = row_pos(live ? row_t : rows - 1, S, H);
