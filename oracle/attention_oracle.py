@@ -43,7 +43,9 @@ Pinning (tests/test_oracle.py): an fp64 closed form (``closed_form``),
 brute-force Python loops on tiny shapes (``brute_force``), and special cases
 the mathematics fixes (S=1, equal keys, causal row 0, window (0,0), one open
 column, zero scale, zero ALiBi slope, RoPE relative-position invariance,
-ALiBi slope closed form).  The reference ships no golden vectors.
+ALiBi slope closed form).  The reference ships no golden vectors; the
+build's own fixtures (tests/golden/: inputs and float64 closed-form answers)
+are checked against this module in tests/test_golden.py.
 
 ``philox4x32_10`` restates the published Philox4x32-10 generator (Salmon et
 al., SC'11) for the kernel's dropout stream; it is pinned to the Random123
