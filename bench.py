@@ -171,14 +171,15 @@ def cold_step_ms(fn, torch, iters=10):
     return sorted(times)[len(times) // 2]
 
 
-def fwd_bwd_ms(w, inp, torch, iters=10):
+def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0):
     """ms of one differentiable step on the workload: forward (with the
-    workload's RoPE) and backward to q, k, v through the HIP kernels."""
+    workload's RoPE) and backward to q, k, v through the HIP kernels, with
+    attention dropout ``dropout_p``."""
     from trinix_amd import triton_attn_func
 
     q, k, v = (t.detach().clone().requires_grad_(True) for t in (inp.q, inp.k, inp.v))
     do = torch.randn_like(inp.q)
-    kw = dict(causal=w.causal, window_size=w.window)
+    kw = dict(causal=w.causal, window_size=w.window, dropout_p=dropout_p)
     if inp.cos is not None:
         kw.update(rotary_cos=inp.cos, rotary_sin=inp.sin)
 
@@ -462,6 +463,10 @@ def main():
         fb = fwd_bwd_ms(w, inp, torch)
         rec["fwd_bwd"] = {"ms": round(fb, 4), "tflops": round(3.5 * fl / fb / 1e9, 2),
                           "bwd_ms": round(fb - ms, 4), "bwd_tflops": round(2.5 * fl / (fb - ms) / 1e9, 2)}
+        # the same step with attention dropout 0.1 (keep masks regenerated
+        # from the forward's Philox stream in both backward kernels)
+        fbd = fwd_bwd_ms(w, inp, torch, dropout_p=0.1)
+        rec["fwd_bwd_dropout"] = {"p": 0.1, "ms": round(fbd, 4), "tflops": round(3.5 * fl / fbd / 1e9, 2)}
     if dname in ("bf16", "fp16") and not args.no_extra:
         del inp
         torch.cuda.empty_cache()

@@ -139,6 +139,21 @@ def test_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
+def test_dropout_backward_is_deterministic_and_follows_the_seed():
+    """The same dropout seed gives bitwise the same gradients; another seed
+    gives other ones."""
+    q, k, v, do = _inputs(1, 200, 200, 4, 2, 128, seed=19)
+    res = []
+    for seed in (77, 77, 78):
+        ts = [t.to(DEV, torch.bfloat16).requires_grad_(True) for t in (q, k, v)]
+        torch.manual_seed(seed)
+        triton_attn_func(*ts, dropout_p=0.2, causal=True).backward(do.to(DEV, torch.bfloat16))
+        res.append([t.grad.clone() for t in ts])
+    for a, b, c in zip(*res):
+        assert torch.equal(a, b)
+        assert not torch.equal(a, c)
+
+
 def test_layer_training_step_gradients():
     torch.manual_seed(21)
     E, H, HKV, S = 256, 4, 2, 96
@@ -228,13 +243,32 @@ def _dropout_grads(q, k, v, do, dtype, keep, p, dev, **kw):
     return out.detach().cpu().double(), [t.grad.cpu().double() for t in ts]
 
 
+def _drop_mask(Sq, Sk, seed):
+    """Additive float mask: -inf on ~20% of 32x32 blocks (never the first key
+    block), N(0, 0.5) elsewhere."""
+    g = torch.Generator().manual_seed(seed)
+    blocks = torch.rand(-(-Sq // 32), -(-Sk // 32), generator=g) < 0.2
+    blocks[:, 0] = False
+    inf = blocks.repeat_interleave(32, 0).repeat_interleave(32, 1)[:Sq, :Sk]
+    return torch.where(inf, float("-inf"), torch.randn(Sq, Sk, generator=g) * 0.5)
+
+
 DROP_CASES = [
-    # (B, Sq, Sk, H, Hkv, D, dtype, p, kwargs)
+    # (B, Sq, Sk, H, Hkv, D, dtype, p, kwargs): bf16/fp16 at head_dim 64/128
+    # run the MFMA pipeline (dK/dV regenerates the keep bits of a key's rows
+    # per quad of lanes, dQ those of a row's keys), fp32 and 256 the generic
+    # kernels
     (1, 160, 160, 4, 2, 64, torch.bfloat16, 0.1, dict(causal=True)),
     (2, 96, 96, 2, 2, 128, torch.float16, 0.3, dict()),
     (1, 128, 128, 4, 1, 128, torch.bfloat16, 0.2, dict(alibi_slopes=orc.alibi_slopes(4), causal=True)),
     (1, 100, 100, 2, 2, 64, torch.float32, 0.25, dict(window_size=(30, 0))),
     (1, 90, 90, 2, 2, 256, torch.bfloat16, 0.1, dict(causal=True)),
+    (1, 130, 200, 4, 2, 128, torch.bfloat16, 0.15, dict(window_size=(50, 20))),
+    (2, 100, 100, 4, 4, 64, torch.float16, 0.5, dict(alibi_slopes=orc.alibi_slopes(4),
+                                                     attn_mask=_drop_mask(100, 100, 31))),
+    (1, 150, 150, 2, 1, 128, torch.bfloat16, 0.1, dict(attn_mask=_drop_mask(150, 150, 32), causal=True)),
+    (1, 17, 17, 1, 1, 128, torch.float16, 0.1, dict(causal=True)),
+    (1, 40, 70, 2, 1, 64, torch.bfloat16, 0.05, dict(softmax_scale=0.2)),
 ]
 
 

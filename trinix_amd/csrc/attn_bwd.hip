@@ -3,9 +3,8 @@
 // trinix_attn_bwd validates the arguments, computes delta = rowsum(dO * O)
 // into the caller's workspace and launches the dK/dV and dQ kernels: the
 // bf16/fp16 MFMA pipeline (attn_bwd16.h, instantiated per (dtype, head_dim)
-// in attn_bwd16_*.hip) for head_dim 64/128 without dropout, the generic
-// fp32-product kernels (attn_bwd_generic.hip) for fp32, head_dim 256 and
-// dropout.
+// in attn_bwd16_*.hip) for head_dim 64/128, dropout included, the generic
+// fp32-product kernels (attn_bwd_generic.hip) for fp32 and head_dim 256.
 #include <cstdint>
 
 #include "attn_bwd16.h"
@@ -112,11 +111,11 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.seed_hi = (uint32_t)(a->dropout_seed >> 32);
   p.off_lo = (uint32_t)a->dropout_offset;
   p.off_hi = (uint32_t)(a->dropout_offset >> 32);
-  const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0);
+  const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0);
 
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;
-  if (a->dtype == TRINIX_F32 || a->head_dim == 256 || p.use_dropout) {
+  if (a->dtype == TRINIX_F32 || a->head_dim == 256) {
     if (!bwd_generic_fits(p)) return TRINIX_ERR_BAD_SHAPE;
     err = launch_bwd_generic(p, a->dtype, (int)a->head_dim, st);
     return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;

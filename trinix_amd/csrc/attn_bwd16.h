@@ -135,6 +135,39 @@ struct TileReader {
   }
 };
 
+// Dropout of the forward (attn_params.h dropout_group), regenerated: (row i,
+// key j) is dropped when word j%4 of Philox(counter (j/4, i, b*Hq+h, off_lo),
+// key (seed_lo ^ off_hi, seed_hi)) is below drop_thresh.
+//
+// keep_bits_of_key: for a lane that owns key j (j % 4 == lane % 4, the four
+// lanes of a quad holding keys 4m..4m+3) and the 16 query rows
+// r0 + (v>>2)*8 + (v&3), v = 0..15, bit v of the result is set when (row v,
+// j) is kept.  The forward draws one Philox call per (row, 4 consecutive
+// keys), so the lanes of a quad share every call: lane e makes the calls of
+// the rows with v&3 == e and the quad swaps the results through DPP quad
+// broadcasts (one call per 4 elements, as in the forward).
+__device__ inline uint32_t keep_bits_of_key(const BwdParams& p, int bh, int j, int r0) {
+  const int e = j & 3;
+  uint32_t own = 0;  // bit vq*4 + k: row r0 + vq*8 + e, key 4*(j/4) + k
+#pragma unroll
+  for (int vq = 0; vq < 4; ++vq) {
+    const u32x4_t c = {(uint32_t)(j >> 2), (uint32_t)(r0 + vq * 8 + e), (uint32_t)bh, p.off_lo};
+    const u32x4_t w = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) own |= (w[k] >= p.drop_thresh ? 1u : 0u) << (vq * 4 + k);
+  }
+  // row v = vq*4 + q of this lane: bit vq*4 + e of quad lane q's `own`
+  // (DPP quad_perm [q,q,q,q] = q * 0x55)
+  const uint32_t o0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0x00, 0xf, 0xf, false);
+  const uint32_t o1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0x55, 0xf, 0xf, false);
+  const uint32_t o2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xaa, 0xf, 0xf, false);
+  const uint32_t o3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xff, 0xf, 0xf, false);
+  return ((o0 >> e) & 0x1111u) | (((o1 >> e) & 0x1111u) << 1) | (((o2 >> e) & 0x1111u) << 2) |
+         (((o3 >> e) & 0x1111u) << 3);
+}
+// All ones when bit v of keep bits m is set, else 0 (one v_bfe_i32).
+__device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int)(m << (31 - v)) >> 31); }
+
 // ---------------------------------------------------------------------------
 // dK, dV: a two-stage pipeline over two wavefronts per 32-key group.  Lane l
 // of either wavefront of group kg owns key j = kb0 + 32kg + l%32.  Per
@@ -155,8 +188,12 @@ struct TileReader {
 // stage B's item, the item being loaded) and P through 2; one barrier per
 // item orders all of it.  The loop runs six steps per trip so that every slot
 // index is a compile-time constant (LDS addresses as immediate offsets).
+// With dropout (DROP), stage A regenerates the keep bits of its sub-tile,
+// takes dV^T += dO^T Pd with Pd = keep ? P/(1-p) : 0, and hands the bits to
+// stage B through LDS next to P; stage B takes dZ = P (keep dP/(1-p) - delta)
+// (delta = rowsum(dO*O) is unchanged by dropout).
 // ---------------------------------------------------------------------------
-template <class E, int D, bool ALIBI, bool MASK>
+template <class E, int D, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   constexpr int NW = 8, NG = NW / 2, BK = NG * 32, BQ = 64, NSL = 3, NST = BQ / 32;
   constexpr int DS = D / 16, DB = D / 32, UPR = D / 8, TILE = BQ * D;
@@ -169,6 +206,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   __shared__ __attribute__((aligned(1024))) u32x4_t lds_p[2 * NG * NST * 2 * 64];
   __shared__ __attribute__((aligned(256))) float lds_l[NSL * BQ];
   __shared__ __attribute__((aligned(256))) float lds_d[NSL * BQ];
+  __shared__ __attribute__((aligned(256))) uint32_t lds_m[DROP ? 2 * NG * NST * 64 : 1];  // keep bits
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -261,6 +299,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   // register layout both stages share
   auto p_slot = [&](int ps, int st, int kk) __attribute__((always_inline)) {
     return lds_p + ((ps * NG + kg) * NST + st) * 2 * 64 + kk * 64 + lane;
+  };
+  // the lane's keep bits of sub-tile st of P slot ps (DROP)
+  auto m_slot = [&](int ps, int st) __attribute__((always_inline)) {
+    return lds_m + ((ps * NG + kg) * NST + st) * 64 + lane;
   };
 
   // One stage: operand rows, the step loop, the epilogue.  Both stages run
@@ -393,6 +435,17 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
                              E::pack(x[kk * 8 + 4], x[kk * 8 + 5]), E::pack(x[kk * 8 + 6], x[kk * 8 + 7])};
           *p_slot(PS, st, kk) = pb[kk];
         }
+        if constexpr (DROP) {
+          // dV takes the dropped, rescaled P of the forward's PV product
+          const uint32_t km = keep_bits_of_key(p, b * p.Hq + hq, j, i0 + st * 32 + g * 4);
+          *m_slot(PS, st) = km;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) x[v] = __uint_as_float(__float_as_uint(x[v] * p.drop_scale) & keep_word(km, v));
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk)
+            pb[kk] = (u32x4_t){E::pack(x[kk * 8 + 0], x[kk * 8 + 1]), E::pack(x[kk * 8 + 2], x[kk * 8 + 3]),
+                               E::pack(x[kk * 8 + 4], x[kk * 8 + 5]), E::pack(x[kk * 8 + 6], x[kk * 8 + 7])};
+        }
         __builtin_amdgcn_s_setprio(1);
         grad(ot_lds, st, pb, t0);
         __builtin_amdgcn_s_setprio(0);
@@ -415,6 +468,13 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         tpre(qt_lds, st, t0);
         __builtin_amdgcn_s_setprio(0);
         u32x4_t zb[2];
+        uint32_t km = 0;
+        if constexpr (DROP) km = *m_slot(PS, st);
+        // dP of the dropped P: keep ? dP/(1-p) : 0 (DROP)
+        auto dpk = [&](int v) __attribute__((always_inline)) {
+          if constexpr (DROP) return __uint_as_float(__float_as_uint(dp[v] * p.drop_scale) & keep_word(km, v));
+          else return dp[v];
+        };
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const u32x4_t pw = *p_slot(PS, st, kk);  // word w: elements kk*8 + 2w, kk*8 + 2w + 1
@@ -423,10 +483,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
           for (int h = 0; h < 2; ++h) {
             const int vq = kk * 2 + h;
             const f32x4_t d4 = *(const f32x4_t*)(d_lds + st * 32 + vq * 8 + g * 4);
-            z[h * 4 + 0] = E::lo(pw[h * 2 + 0]) * (dp[vq * 4 + 0] - d4[0]);
-            z[h * 4 + 1] = E::hi(pw[h * 2 + 0]) * (dp[vq * 4 + 1] - d4[1]);
-            z[h * 4 + 2] = E::lo(pw[h * 2 + 1]) * (dp[vq * 4 + 2] - d4[2]);
-            z[h * 4 + 3] = E::hi(pw[h * 2 + 1]) * (dp[vq * 4 + 3] - d4[3]);
+            z[h * 4 + 0] = E::lo(pw[h * 2 + 0]) * (dpk(vq * 4 + 0) - d4[0]);
+            z[h * 4 + 1] = E::hi(pw[h * 2 + 0]) * (dpk(vq * 4 + 1) - d4[1]);
+            z[h * 4 + 2] = E::lo(pw[h * 2 + 1]) * (dpk(vq * 4 + 2) - d4[2]);
+            z[h * 4 + 3] = E::hi(pw[h * 2 + 1]) * (dpk(vq * 4 + 3) - d4[3]);
           }
           zb[kk] = (u32x4_t){E::pack(z[0], z[1]), E::pack(z[2], z[3]), E::pack(z[4], z[5]), E::pack(z[6], z[7])};
         }
@@ -492,9 +552,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 // i = m0 + 32w + l%32; per 64-key tile S^T = K Q^T and dP^T = V dO^T (keys on
 // the MFMA rows, A operands from the K / V tiles in LDS; B operands the
 // lane's Q / dO rows in registers), dZ^T = P^T (dP^T - delta) in registers,
-// dQ^T += K^T dZ^T with K^T from LDS transpose reads.
+// dQ^T += K^T dZ^T with K^T from LDS transpose reads.  With dropout (DROP)
+// dZ = P (keep dP/(1-p) - delta); a lane's 4 consecutive keys vq*8 + 4g +
+// 0..3 of a 32-key half are one Philox call of the forward's stream.
 // ---------------------------------------------------------------------------
-template <class E, int D, bool ALIBI, bool MASK>
+template <class E, int D, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
   constexpr int NW = 4, BM = NW * 32, BN = 64;
   constexpr int DS = D / 16, DB = D / 32, NB = BN / 32, UPR = D / 8;
@@ -652,8 +714,22 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
       u32x4_t zb[2];
       {
         float z[16];
+        if constexpr (DROP) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dp[v] - dlt);
+          for (int vq = 0; vq < 4; ++vq) {
+            const int jq = n0 + nb * 32 + vq * 8 + g * 4;
+            const u32x4_t c = {(uint32_t)(jq >> 2), (uint32_t)i, (uint32_t)(b * p.Hq + hq), p.off_lo};
+            const u32x4_t w = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float dpk = w[e] < p.drop_thresh ? 0.f : dp[vq * 4 + e] * p.drop_scale;
+              z[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - lse2) * (dpk - dlt);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dp[v] - dlt);
+        }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
           zb[kk] = (u32x4_t){E::pack(z[kk * 8 + 0], z[kk * 8 + 1]), E::pack(z[kk * 8 + 2], z[kk * 8 + 3]),
@@ -721,24 +797,29 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
   }
 }
 
-// Launch of both gradient kernels for one (dtype, D); feat = kFeatAlibi | kFeatMask.
+// Launch of both gradient kernels for one (dtype, D); feat = kFeatAlibi |
+// kFeatMask | kFeatDropout.
 template <class E, int D>
 hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
   const dim3 g_kv((unsigned)(p.B * p.Hkv * p.num_kblk)), g_q((unsigned)(p.B * p.Hq * p.num_mblk)), blk(256),
       blk_kv(512);
-  switch (feat & 3) {
-#define TRINIX_BWD_CASE(F)                                                                                        \
-  case F:                                                                                                         \
-  {                                                                                                               \
-    const hipError_t e = launch_kernel(&attn_bwd_dkdv<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>, g_kv,   \
-                                       blk_kv, 0, st, p);                                                          \
-    if (e != hipSuccess) return e;                                                                                \
-    return launch_kernel(&attn_bwd_dq<E, D, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0>, g_q, blk, 0, st, p);     \
+  switch (feat & 7) {
+#define TRINIX_BWD_CASE(F)                                                                                \
+  case F:                                                                                                 \
+  {                                                                                                       \
+    constexpr bool A = (F & kFeatAlibi) != 0, M = (F & kFeatMask) != 0, DR = (F & kFeatDropout) != 0;     \
+    const hipError_t e = launch_kernel(&attn_bwd_dkdv<E, D, A, M, DR>, g_kv, blk_kv, 0, st, p);           \
+    if (e != hipSuccess) return e;                                                                        \
+    return launch_kernel(&attn_bwd_dq<E, D, A, M, DR>, g_q, blk, 0, st, p);                               \
   }
     TRINIX_BWD_CASE(0)
     TRINIX_BWD_CASE(1)
     TRINIX_BWD_CASE(2)
     TRINIX_BWD_CASE(3)
+    TRINIX_BWD_CASE(4)
+    TRINIX_BWD_CASE(5)
+    TRINIX_BWD_CASE(6)
+    TRINIX_BWD_CASE(7)
 #undef TRINIX_BWD_CASE
   }
   return hipErrorNotSupported;

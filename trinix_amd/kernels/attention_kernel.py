@@ -43,7 +43,8 @@ _MASK_DTYPE_CODE = {
 }
 KERNEL_HEAD_DIMS = (64, 128, 256)
 # The backward kernels are built for the same widths (bf16/fp16 at 64 and
-# 128 without dropout run the MFMA pipeline, the rest the generic kernels).
+# 128 run the MFMA pipeline, dropout included; fp32 and 256 the generic
+# kernels).
 BACKWARD_HEAD_DIMS = (64, 128, 256)
 
 
