@@ -184,8 +184,10 @@ int main() {
     const int rc = validate_fwd_args(&a);
     if (rc != TRINIX_OK) continue;
     ++accepted;
-    const Cfg16 c = pick_cfg16(a.head_dim, a.batch, a.nheads_q, a.seqlen_q);
-    CHECK(c.nw == 4 && c.bn == 64 && (c.ks == 1 || c.ks == 2), "tile config");
+    const bool plain = !a.mask && a.dropout_p == 0.f;
+    const Cfg16 c = pick_cfg16(a.head_dim, a.batch, a.nheads_q, a.seqlen_q, a.causal || a.has_window, plain);
+    CHECK((c.nw == 4 && c.bn == 64 && (c.ks == 1 || c.ks == 2)) ||
+              (c.nw == 8 && c.bn == 128 && c.ks == 1 && a.head_dim == 128 && plain), "tile config");
     SplitPlan pl;
     if (make_split_plan(&a, &pl)) {
       ++planned;

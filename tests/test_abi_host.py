@@ -68,6 +68,8 @@ def test_version_status_and_tiles(lib):
     cfg = nat.TileCfg()
     assert lib.trinix_attn_tile_config(128, nat.TRINIX_BF16, ctypes.byref(cfg)) == 0
     assert cfg.block_d == 128 and cfg.block_m % 32 == 0 and cfg.block_n % 64 == 0
+    # large problems at head_dim 128: 8 wavefronts x 32 rows, 128-key tiles
+    assert (cfg.block_m, cfg.block_n, cfg.waves, cfg.lds_bytes) == (256, 128, 8, 2 * 2 * 128 * 128 * 2)
     assert lib.trinix_attn_tile_config(96, nat.TRINIX_BF16, ctypes.byref(cfg)) == nat.TRINIX_ERR_BAD_HEAD_DIM
     assert lib.trinix_attn_tile_config(256, nat.TRINIX_BF16, ctypes.byref(cfg)) == 0
     assert cfg.block_d == 256 and cfg.lds_bytes == 4 * 64 * 256 * 2

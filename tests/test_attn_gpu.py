@@ -555,3 +555,76 @@ def test_key_split_configs(case, dtype, monkeypatch):
     fin = torch.isfinite(l1)
     assert torch.equal(fin, torch.isfinite(l2))
     assert (l1[fin] - l2[fin]).abs().max().item() <= 1e-2
+
+
+WIDE_CASES = [
+    # (B, Sq, Sk, H, Hkv, causal, window, features), head_dim 128
+    (1, 300, 300, 4, 2, True, None, ""),
+    (2, 200, 333, 4, 4, False, None, "alibi"),
+    (1, 520, 520, 2, 1, True, (100, 0), ""),
+    (1, 64, 700, 2, 2, False, (50, 60), ""),
+    (1, 257, 257, 4, 4, True, None, "rope,qn"),
+    (1, 1000, 1000, 2, 2, True, None, "alibi,qn"),
+    (1, 130, 600, 2, 1, True, None, "rope"),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", WIDE_CASES, ids=[str(c) for c in WIDE_CASES])
+def test_wide_tile_config(case, dtype, monkeypatch):
+    """Head_dim 128 without a mask or dropout runs 256-row workgroups with
+    128-key tiles once the grid is large (C3, C4).  Forced here through
+    TRINIX_ATTN_CFG on small problems (partial tiles, Sq != Sk, windows,
+    GQA/MQA, ALiBi, fused RoPE and q RMSNorm): output and lse against the
+    oracle, and against the 128-row, 64-key shape."""
+    B, Sq, Sk, H, Hkv, causal, window, feats = case
+    D = 128
+    q, k, v = rand((B, Sq, H, D), dtype, 111), rand((B, Sk, Hkv, D), dtype, 112), rand((B, Sk, Hkv, D), dtype, 113)
+    kw = dict(causal=causal, window_size=window)
+    if "alibi" in feats:
+        kw["alibi_slopes"] = orc.alibi_slopes(H)
+    dkw = {a: (b.to(DEV) if torch.is_tensor(b) else b) for a, b in kw.items()}
+    qr, kr, eps = q.cpu(), k.cpu(), 1e-5
+    if "rope" in feats:
+        cos, sin = orc.rope_tables(max(Sq, Sk), D, 10000.0, dtype)
+        dkw.update(rotary_cos=cos.to(DEV), rotary_sin=sin.to(DEV))
+        qr, kr = orc.apply_rope(qr, cos, sin), orc.apply_rope(kr, cos, sin)
+    if "qn" in feats:
+        w = (1.0 + 0.3 * torch.randn(D, generator=torch.Generator().manual_seed(114))).to(dtype)
+        dkw.update(q_norm_weight=w.to(DEV), q_norm_eps=eps)
+        qr = orc.qk_rms_norm(qr, w, eps)
+    outs = {}
+    for cfg in ("4,2,64,1", "8,2,128,1"):
+        monkeypatch.setenv("TRINIX_ATTN_CFG", cfg)
+        outs[cfg] = TritonAttentionKernel.apply(q, k, v, return_lse=True, **dkw)
+    monkeypatch.delenv("TRINIX_ATTN_CFG")
+    ref = oracle_on(qr, kr, v, **kw)
+    x64 = orc.closed_form(qr, kr, v.cpu(), **kw)
+    for cfg, (out, _) in outs.items():
+        assert_parity_or_more_accurate(out, ref, x64, dtype, f"{case} {cfg}")
+    (o1, l1), (o2, l2) = outs.values()
+    ok = ~torch.isnan(o1.float())
+    assert torch.equal(torch.isnan(o1), torch.isnan(o2))
+    assert (o1.float() - o2.float()).abs()[ok].max().item() <= 2e-2
+    fin = torch.isfinite(l1)
+    assert torch.equal(fin, torch.isfinite(l2))
+    assert (l1[fin] - l2[fin]).abs().max().item() <= 1e-2
+
+
+def test_wide_tile_config_chosen_for_large_grids(monkeypatch):
+    """The planner's choice: 256-row, 128-key workgroups at head_dim 128 for
+    C3-sized grids without a mask or dropout; the 128-row shape for small
+    causal grids, with a mask, and at head_dim 64 (checked through the
+    forced-config error: a shape that is not built for a call is rejected)."""
+    from trinix_amd.kernels import tile_config
+
+    cfg = tile_config(128, torch.bfloat16)
+    assert (cfg["block_m"], cfg["block_n"], cfg["waves"]) == (256, 128, 8)
+    q = rand((1, 64, 2, 128), torch.bfloat16, 5)
+    m = torch.zeros(64, 64, device=DEV)
+    monkeypatch.setenv("TRINIX_ATTN_CFG", "8,2,128,1")
+    with pytest.raises((ValueError, RuntimeError)):
+        TritonAttentionKernel.apply(q, q, q, attn_mask=m)  # no mask kernels at this shape
+    q64 = rand((1, 64, 2, 64), torch.bfloat16, 6)
+    with pytest.raises((ValueError, RuntimeError)):
+        TritonAttentionKernel.apply(q64, q64, q64)

@@ -301,7 +301,7 @@ int trinix_attn_tile_config(int64_t head_dim, int32_t dtype, trinix_tile_cfg* ou
   if (!out) return TRINIX_ERR_NULL_POINTER;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
   if (dtype == TRINIX_BF16 || dtype == TRINIX_F16) {
-    const Cfg16 c = pick_cfg16(head_dim, 1 << 20, 1, 1 << 20);  // large-problem choice
+    const Cfg16 c = pick_cfg16(head_dim, 1 << 20, 1, 1 << 20, true, true);  // large-problem choice
     out->block_m = 32 * c.nw / c.ks;
     out->block_n = c.bn;
     out->block_d = (int32_t)head_dim;
@@ -340,7 +340,8 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.Hkv = (int)a->nheads_kv;
   p.G = p.Hq / p.Hkv;
   const bool f32 = a->dtype == TRINIX_F32;
-  Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q);
+  Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q, a->causal || a->has_window,
+                         !a->mask && !(a->dropout_p > 0.f));
   if (a->q_norm_weight) cfg.ks = 1;  // the fused q RMSNorm is built without the key split
   const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw / cfg.ks;
   p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);

@@ -744,15 +744,43 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
   return hipErrorNotSupported;
 }
 
+// Launcher of a tile shape built only for calls without a mask or dropout
+// (ALiBi and the fused q RMSNorm included): the 128-key tiles at D = 128,
+// whose mask and dropout variants would spill.
+template <class E, int D, int BN, int NW, int OCC, int KS>
+hipError_t launch_feat_plain(const FwdParams& p, int feat, hipStream_t st) {
+  const dim3 grid((unsigned)p.total_work), block(NW * 64);
+  switch (feat) {
+#define TRINIX_CASE(F)                                                                                          \
+  case F:                                                                                                       \
+    return launch_kernel(&attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, false, false,         \
+                                          (F & kFeatQNorm) != 0>,                                              \
+                         grid, block, 0, st, p);
+    TRINIX_CASE(0)
+    TRINIX_CASE((kFeatAlibi))
+    TRINIX_CASE((kFeatQNorm))
+    TRINIX_CASE((kFeatQNorm | kFeatAlibi))
+    default:
+      break;
+#undef TRINIX_CASE
+  }
+  return hipErrorNotSupported;
+}
+
 // Tile configs built per (dtype, D), every feature combination:
 // (nw, occ, bn, ks) = (4, 2, 64, 1) for D <= 128; (4, 1, 64, 1) for D = 256,
 // whose Q fragment (64 VGPRs) and O accumulator (128) need one wavefront per
 // SIMD, and whose double-buffered K/V tiles take 128 KiB of LDS; and for D = 64
 // also (4, 2, 64, 2), the key split for small grids (64 KiB of LDS: two
-// tiles per buffer).
+// tiles per buffer).  For D = 128 without a mask or dropout also (8, 2, 128,
+// 1): 256 rows and 128-key tiles per workgroup (128 KiB of LDS, one
+// workgroup per CU).
 #define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                                   \
   hipError_t NAME(const FwdParams& p, Cfg16 cfg, int feat, hipStream_t st) {                                \
     constexpr int kOcc = (D) == 256 ? 1 : 2;                                                               \
+    if constexpr ((D) == 128)                                                                              \
+      if (cfg.nw == 8 && cfg.bn == 128 && cfg.occ == 2 && cfg.ks == 1)                                     \
+        return launch_feat_plain<E, D, 128, 8, 2, 1>(p, feat, st);                                         \
     if (cfg.bn != 64 || cfg.nw != 4 || cfg.occ != kOcc) return hipErrorNotSupported;                       \
     if (cfg.ks == 1) return launch_feat<E, D, 64, 4, kOcc, 1>(p, feat, st);                                \
     if constexpr ((D) == 64)                                                                               \

@@ -52,13 +52,24 @@ int check16(const void* ptr, const int64_t st[4]) {
 // the workgroups, half the longest chain of tiles, at twice the K/V copies
 // per flop.  Measured at head_dim 64, bf16: 128 workgroups at S = 4096..16384
 // +50..62%, 64 workgroups at S = 1024 +2%, 384 workgroups (S = 1024) -3%.
+// Head_dim 128 without a mask or dropout takes 8 wavefronts x 32 rows and
+// 128-key tiles (one workgroup of 256 rows per CU, 128 KiB of LDS): half the
+// barriers and tile bookkeeping per flop, once the grid holds enough 256-row
+// workgroups -- 512 with causal / window bands (whose rows differ in length),
+// 256 without.  Measured at bf16, graph-timed kernel: causal 512 workgroups
+// +8%, 1024 +1.5..3% (C3), 2048 +2.7%, C4 +2..2.4%; full rows 256 workgroups
+// +8%; below those counts it loses (causal 256 workgroups -9%, 128 -20%).
 // TRINIX_ATTN_CFG="nw,occ,bn[,ks]" overrides the choice (tuning only; a
 // configuration that is not built is rejected with TRINIX_ERR_BAD_ARGUMENT).
 constexpr int64_t kSmallGrid = 256;  // CUs of an MI355X
-Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq) {
+Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain) {
   Cfg16 c{4, head_dim == 256 ? 1 : 2, 64, 1};
   // batch * hq * row blocks, without overflow (each factor < 2^31 here)
   if (head_dim == 64 && batch * hq <= kSmallGrid && batch * hq * ((sq + 127) / 128) <= kSmallGrid) c.ks = 2;
+  if (head_dim == 128 && plain) {
+    const int64_t need = banded ? 2 * kSmallGrid : kSmallGrid;
+    if (batch * hq >= need || batch * hq * ((sq + 255) / 256) >= need) c = Cfg16{8, 2, 128, 1};
+  }
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
     int nw = 0, occ = 0, bn = 0, ks = 1;
     if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &ks) >= 3 && nw > 0 && ks > 0 && nw % ks == 0)

@@ -25,8 +25,9 @@ constexpr int64_t kMaxKvRowStride = 1ll << 22;
 int validate_fwd_args(const trinix_attn_fwd_args* a);
 int validate_bwd_args(const trinix_attn_bwd_args* a);
 
-// Tile configuration of the 16-bit forward for a problem.
-Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq);
+// Tile configuration of the 16-bit forward for a problem: `banded` when
+// causal or windowed, `plain` without a mask or dropout.
+Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain);
 
 // Split-KV decode plan.
 constexpr int kDecodeMaxSq = 16;
