@@ -207,7 +207,10 @@ int main() {
     a.dtype = (int32_t)(next_u64() % 4);
     for (int i = 0; i < 4; ++i)
       if (next_u64() % 4 == 0) a.dk_stride[i] = rand_size();
-    (void)validate_bwd_args(&a);
+    if (validate_bwd_args(&a) != TRINIX_OK) continue;
+    const bool masked = next_u64() % 2 == 0;
+    if (pick_dq_wide(a.head_dim, a.batch, a.nheads_q, a.seqlen_q, a.causal || a.has_window, masked))
+      CHECK(a.head_dim == 128 && !masked, "wide dQ only at head_dim 128 without a mask");
   }
   std::printf("cases %d, fuzz accepted %d, planned %d, failures %d\n", cases, accepted, planned, failures);
   if (failures) return 1;

@@ -139,6 +139,35 @@ def test_backward_is_deterministic():
         assert torch.equal(a, b)
 
 
+WIDE_DQ_CASES = [
+    # (B, Sq, Sk, H, Hkv, dtype, kwargs), head_dim 128
+    (1, 300, 300, 4, 2, torch.bfloat16, dict(causal=True)),
+    (2, 130, 250, 2, 2, torch.float16, dict(window_size=(60, 20), alibi_slopes=orc.alibi_slopes(2))),
+    (1, 200, 200, 4, 1, torch.bfloat16, dict(causal=True, dropout_p=0.2)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(WIDE_DQ_CASES)))
+def test_wide_dq_shape(case, monkeypatch):
+    """The dQ kernel's 256-row, 128-key shape (taken on large grids at head_dim
+    128 without a mask), forced through TRINIX_BWD_DQ_WIDE: bitwise the
+    gradients of the 128-row shape (the same per-row order of key tiles),
+    and within the bar against fp64 autograd."""
+    B, Sq, Sk, H, Hkv, dtype, kw = WIDE_DQ_CASES[case]
+    q, k, v, do = _inputs(B, Sq, Sk, H, Hkv, 128, seed=700 + case)
+    grads = {}
+    for wide in ("0", "1"):
+        monkeypatch.setenv("TRINIX_BWD_DQ_WIDE", wide)
+        torch.manual_seed(99)  # the same dropout seed in both runs
+        grads[wide] = _hip_grads(q, k, v, do, dtype, **kw)[1]
+    for a, b in zip(grads["0"], grads["1"]):
+        assert torch.equal(a, b)
+    if "dropout_p" not in kw:
+        _, truth = _eager_grads(q, k, v, do, torch.float64, **kw)
+        _, eager = _eager_grads(q, k, v, do, dtype, **kw)
+        _check(grads["1"], eager, truth)
+
+
 def test_dropout_backward_is_deterministic_and_follows_the_seed():
     """The same dropout seed gives bitwise the same gradients; another seed
     gives other ones."""

@@ -98,7 +98,9 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.bm_sh = a->blockmap_stride[1];
   p.bm_cols = (int)((a->seqlen_k + 63) / 64);
   p.num_kblk = (int)((a->seqlen_k + 127) / 128);
-  p.num_mblk = (int)((a->seqlen_q + 127) / 128);
+  p.dq_wide = a->dtype != TRINIX_F32 && pick_dq_wide(a->head_dim, a->batch, a->nheads_q, a->seqlen_q,
+                                                      a->causal || a->has_window, a->mask != nullptr) ? 1 : 0;
+  p.num_mblk = (int)((a->seqlen_q + (p.dq_wide ? 255 : 127)) / (p.dq_wide ? 256 : 128));
   if ((int64_t)p.B * p.Hq * p.num_mblk >= (1ll << 31) || (int64_t)p.B * p.Hkv * p.num_kblk >= (1ll << 31))
     return TRINIX_ERR_BAD_SHAPE;
   p.use_dropout = a->dropout_p > 0.f ? 1 : 0;

@@ -16,7 +16,9 @@
 //              and every query tile of the band, so dK and dV of a KV head
 //              are summed in registers (GQA included);
 //   bwd_dq     one workgroup per (batch, q-head, 128 query rows), the
-//              forward's shape: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T.
+//              forward's shape: S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dZ^T;
+//              at head_dim 128 without a mask on large grids, 256 rows and
+//              128-key tiles per workgroup (dq_wide, as the forward).
 // All products run on v_mfma_f32_32x32x16_{bf16,f16}; P and dZ are rounded to
 // the input dtype for their products, as in the forward.  bwd_dkdv also takes
 // dZ = P (dP - delta) from the rounded P (bwd_dq from the fp32 one).
@@ -54,7 +56,8 @@ struct BwdParams {
   const uint8_t* bmap;
   int64_t bm_sb, bm_sh;
   int bm_cols;
-  int num_kblk, num_mblk;  // 128-key blocks (dK/dV), 128-row blocks (dQ)
+  int num_kblk, num_mblk;  // 128-key blocks (dK/dV), 128- or 256-row blocks (dQ)
+  int dq_wide;             // dQ in 256-row workgroups with 128-key tiles
   // dropout of the forward (attn_params.h dropout_group): same Philox stream
   int use_dropout;
   uint32_t drop_thresh;  // dropped when the Philox word < drop_thresh
@@ -549,16 +552,17 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // dQ.  The forward's decomposition: lane l of wavefront w owns query row
-// i = m0 + 32w + l%32; per 64-key tile S^T = K Q^T and dP^T = V dO^T (keys on
+// i = m0 + 32w + l%32 (NW wavefronts, BN-key tiles: 4 and 64, or 8 and 128
+// with dq_wide); per 32-key half of a tile S^T = K Q^T and dP^T = V dO^T (keys on
 // the MFMA rows, A operands from the K / V tiles in LDS; B operands the
 // lane's Q / dO rows in registers), dZ^T = P^T (dP^T - delta) in registers,
 // dQ^T += K^T dZ^T with K^T from LDS transpose reads.  With dropout (DROP)
 // dZ = P (keep dP/(1-p) - delta); a lane's 4 consecutive keys vq*8 + 4g +
 // 0..3 of a 32-key half are one Philox call of the forward's stream.
 // ---------------------------------------------------------------------------
-template <class E, int D, bool ALIBI, bool MASK, bool DROP>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq(const BwdParams p) {
-  constexpr int NW = 4, BM = NW * 32, BN = 64;
+template <class E, int D, bool ALIBI, bool MASK, bool DROP, int NW, int BN>
+__global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
+  constexpr int BM = NW * 32;
   constexpr int DS = D / 16, DB = D / 32, NB = BN / 32, UPR = D / 8;
   constexpr int LPW = BN * UPR / (64 * NW);
 
@@ -810,7 +814,9 @@ hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
     constexpr bool A = (F & kFeatAlibi) != 0, M = (F & kFeatMask) != 0, DR = (F & kFeatDropout) != 0;     \
     const hipError_t e = launch_kernel(&attn_bwd_dkdv<E, D, A, M, DR>, g_kv, blk_kv, 0, st, p);           \
     if (e != hipSuccess) return e;                                                                        \
-    return launch_kernel(&attn_bwd_dq<E, D, A, M, DR>, g_q, blk, 0, st, p);                               \
+    if constexpr (D == 128 && !M)                                                                         \
+      if (p.dq_wide) return launch_kernel(&attn_bwd_dq<E, D, A, M, DR, 8, 128>, g_q, blk_kv, 0, st, p);    \
+    return launch_kernel(&attn_bwd_dq<E, D, A, M, DR, 4, 64>, g_q, blk, 0, st, p);                        \
   }
     TRINIX_BWD_CASE(0)
     TRINIX_BWD_CASE(1)

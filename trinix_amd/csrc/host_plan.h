@@ -28,6 +28,8 @@ int validate_bwd_args(const trinix_attn_bwd_args* a);
 // Tile configuration of the 16-bit forward for a problem: `banded` when
 // causal or windowed, `plain` without a mask or dropout.
 Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain);
+// Whether the 16-bit dQ backward runs 256-row workgroups with 128-key tiles.
+bool pick_dq_wide(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool masked);
 
 // Split-KV decode plan.
 constexpr int kDecodeMaxSq = 16;
