@@ -185,9 +185,22 @@ int main() {
     if (rc != TRINIX_OK) continue;
     ++accepted;
     const bool plain = !a.mask && a.dropout_p == 0.f;
-    const Cfg16 c = pick_cfg16(a.head_dim, a.batch, a.nheads_q, a.seqlen_q, a.causal || a.has_window, plain);
+    const bool split_ok = plain && a.causal && !a.has_window;
+    const Cfg16 c = pick_cfg16(a.head_dim, a.batch, a.nheads_q, a.seqlen_q, a.causal || a.has_window, plain,
+                               split_ok);
     CHECK((c.nw == 4 && c.bn == 64 && (c.ks == 1 || c.ks == 2)) ||
+              (c.nw == 4 && c.bn == 64 && c.ks == 0 && a.head_dim == 64 && split_ok) ||
               (c.nw == 8 && c.bn == 128 && c.ks == 1 && a.head_dim == 128 && plain), "tile config");
+    if (c.ks == 0) {
+      uint8_t items[kMaxRowItems];
+      const int n = plan_split_rows(a.seqlen_q, a.seqlen_k, a.batch * a.nheads_q, 128, 64, items, kMaxRowItems);
+      CHECK(n >= 0 && n <= kMaxRowItems, "split items");
+      // every 128-row block appears once whole or as both halves
+      int seen[64] = {0};
+      for (int k = 0; k < n; ++k) seen[items[k] >> 2] += (items[k] & 2) ? 1 : 2;
+      const int64_t nb = (a.seqlen_q + 127) / 128;
+      for (int64_t rb = 0; n > 0 && rb < nb; ++rb) CHECK(seen[rb] == 2, "split items cover every row block");
+    }
     SplitPlan pl;
     if (make_split_plan(&a, &pl)) {
       ++planned;

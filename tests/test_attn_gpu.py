@@ -611,6 +611,43 @@ def test_wide_tile_config(case, dtype, monkeypatch):
     assert (l1[fin] - l2[fin]).abs().max().item() <= 1e-2
 
 
+SPLIT_CASES = [
+    # (B, Sq, Sk, H, Hkv, features), head_dim 64, causal
+    (2, 1024, 1024, 12, 12, ""),   # blocks 4..7 split into 64-row halves, 0..3 whole
+    (1, 700, 700, 6, 3, "alibi"),
+    (1, 1000, 1200, 4, 2, ""),     # Sq != Sk
+    (1, 300, 300, 4, 4, ""),       # the last block partial
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[str(c) for c in SPLIT_CASES])
+def test_split_rows_config(case, dtype, monkeypatch):
+    """The per-item key split at head_dim 64 (C2's default: the longest
+    causal row blocks run as two 64-row items with two wavefronts per 32-row
+    group, the others whole), forced through TRINIX_ATTN_CFG: output and lse
+    against the oracle and against the unsplit shape."""
+    B, Sq, Sk, H, Hkv, feats = case
+    D = 64
+    q, k, v = rand((B, Sq, H, D), dtype, 121), rand((B, Sk, Hkv, D), dtype, 122), rand((B, Sk, Hkv, D), dtype, 123)
+    kw = dict(causal=True)
+    if "alibi" in feats:
+        kw["alibi_slopes"] = orc.alibi_slopes(H)
+    dkw = {a: (b.to(DEV) if torch.is_tensor(b) else b) for a, b in kw.items()}
+    outs = {}
+    for cfg in ("4,2,64,1", "4,2,64,0"):
+        monkeypatch.setenv("TRINIX_ATTN_CFG", cfg)
+        outs[cfg] = TritonAttentionKernel.apply(q, k, v, return_lse=True, **dkw)
+    monkeypatch.delenv("TRINIX_ATTN_CFG")
+    ref = oracle_on(q, k, v, **kw)
+    x64 = orc.closed_form(q.cpu(), k.cpu(), v.cpu(), **kw)
+    for cfg, (out, _) in outs.items():
+        assert_parity_or_more_accurate(out, ref, x64, dtype, f"{case} {cfg}")
+    (o1, l1), (o2, l2) = outs.values()
+    assert (o1.float() - o2.float()).abs().max().item() <= 2e-2
+    assert (l1 - l2).abs().max().item() <= 1e-2
+
+
 def test_wide_tile_config_chosen_for_large_grids(monkeypatch):
     """The planner's choice: 256-row, 128-key workgroups at head_dim 128 for
     C3-sized grids without a mask or dropout; the 128-row shape for small

@@ -47,9 +47,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // KS = 2 splits each 32-row group's keys between two wavefronts: wavefront
   // 2r + kp owns rows 32r..32r+31 and the tiles t_lo + KS*s + kp; the halves
   // merge through LDS at the end.  It halves the longest dependency chain of
-  // small problems (few row blocks, long causal rows).
-  static_assert(KS == 1 || KS == 2, "key split");
-  constexpr int BM = NW * 32 / KS;  // query rows per workgroup
+  // small problems (few row blocks, long causal rows).  KS = 0 decides per
+  // work item (p.row_items): the long causal row blocks run split, as two
+  // items of NW*16 rows, the short ones whole (NW*32 rows), so that no item's
+  // chain of tiles is much longer than the others'.
+  static_assert(KS == 0 || KS == 1 || KS == 2, "key split");
+  constexpr int KSL = KS ? KS : 2;  // tiles per LDS buffer
   constexpr int DS = D / 16;   // MFMA k-steps over head_dim (QK^T)
   constexpr int NB = BN / 32;  // 32-key blocks per tile
   constexpr int DB = D / 32;   // 32-wide head_dim blocks of O^T
@@ -62,11 +65,12 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // Four separate LDS objects (not one array indexed by parity) so that the
   // compiler can tell the buffer being read from the one an asynchronous
   // global->LDS load is filling, and does not wait for that load.
-  // With KS = 2 each buffer holds the step's two tiles (tile kp at kp*BN*D).
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_k0[KS * BN * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[KS * BN * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[KS * BN * D];
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[KS * BN * D];
+  // With a key split each buffer holds the step's two tiles (tile kp at
+  // kp*BN*D).
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k0[KSL * BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[KSL * BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[KSL * BN * D];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[KSL * BN * D];
   // Tile t lives in buffer slot (t - t_lo) & 1 of K and of V.  `slot` is a
   // std::integral_constant in the full-tile loop (static buffer choice) and
   // an int in the edge loops.
@@ -82,7 +86,6 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int r = lane & 31, g = lane >> 5;
-  const int kp = wave % KS;  // key parity of this wavefront (KS = 2)
 
   // work item: (b, kv-head, m-block, q-head within the group).  Each XCD owns
   // whole KV-head groups, so the q-heads sharing a KV head run on one XCD and
@@ -111,16 +114,26 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     b = w / p.Hkv;
   }
   const int hq = hkv * p.G + gq;
-  const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
-  const int m0 = mblk * BM;
-  const int iw0 = m0 + (wave / KS) * 32;
+  // ks: wavefronts per 32-row group (1 or 2); bm: rows of the work item
+  int ks = KS, m0;
+  if constexpr (KS == 0) {
+    const uint32_t item = p.row_items[mi];  // row block << 2 | split << 1 | half
+    ks = (item & 2u) ? 2 : 1;
+    m0 = (int)(item >> 2) * (NW * 32) + (int)(item & 1u) * (NW * 16);
+  } else {
+    const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
+    m0 = mblk * (NW * 32 / KS);
+  }
+  const int bm = NW * 32 / ks;
+  const int kp = wave % ks;  // key parity of this wavefront (key split)
+  const int iw0 = m0 + (wave / ks) * 32;
   const int iwl = min(iw0 + 31, p.Sq - 1);
   const int i = iw0 + r;
   const int ic = min(i, p.Sq - 1);
   const bool wave_live = iw0 < p.Sq;
 
   // Key tiles the workgroup visits, and the sub-range of full tiles.
-  const int mlast = min(m0 + BM, p.Sq) - 1;
+  const int mlast = min(m0 + bm, p.Sq) - 1;
   int64_t lo = 0, hi = p.Sk, flo = 0, fhi = p.Sk;
   if (p.causal) {
     hi = min(hi, (int64_t)mlast + 1);
@@ -583,7 +596,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   };
 
   // ---- main loop -----------------------------------------------------------
-  // Step s covers tiles T = t_lo + KS*s .. T + KS - 1 (this wavefront's tile
+  // Step s covers tiles T = t_lo + ks*s .. T + ks - 1 (this wavefront's tile
   // is T + kp), held in buffer slot s & 1 of K and V.  Step s: wait for the
   // step's tiles; barrier (every wavefront done with step s-1, whose buffers
   // now take the loads of step s+1); S = K Q^T; softmax; O += V^T P.
@@ -598,10 +611,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     __builtin_amdgcn_s_waitcnt(0);  // this wavefront's loads of the step's tiles landed
     __syncthreads();                // ... and every wavefront's; buffers of step s-1 are free
 #pragma unroll
-    for (int u = 0; u < KS; ++u)
-      if (T + KS + u < t_hi) {
-        load_k(kbuf(other) + u * BN * D, T + KS + u);
-        load_v(vbuf(other) + u * BN * D, T + KS + u);
+    for (int u = 0; u < ks; ++u)
+      if (T + ks + u < t_hi) {
+        load_k(kbuf(other) + u * BN * D, T + ks + u);
+        load_v(vbuf(other) + u * BN * D, T + ks + u);
       }
     if (t < t_hi && tile_live(t)) {
       const int n0 = t * BN;
@@ -628,7 +641,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   if constexpr (MASK && D <= 128)
     if (bm_row) bm_fetch((t_lo + kp) * NCB);
 #pragma unroll
-  for (int u = 0; u < KS; ++u)
+  for (int u = 0; u < ks; ++u)
     if (t_lo + u < t_hi) {
       load_k(kbuf(std::integral_constant<int, 0>{}) + u * BN * D, t_lo + u);
       load_v(vbuf(std::integral_constant<int, 0>{}) + u * BN * D, t_lo + u);
@@ -637,27 +650,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   // starting at an even step so that their buffer slots are static (the full
   // range is trimmed to start at an even step and to an even length; trimmed
   // steps run the edge body, which is always exact).
-  const int s_hi = (t_hi - t_lo + KS - 1) / KS;
-  int s_flo = (t_flo - t_lo + KS - 1) / KS;
-  int s_fhi = max(s_flo, (t_fhi - t_lo) / KS);
+  const int s_hi = (t_hi - t_lo + ks - 1) / ks;
+  int s_flo = (t_flo - t_lo + ks - 1) / ks;
+  int s_fhi = max(s_flo, (t_fhi - t_lo) / ks);
   if ((s_flo & 1) && s_flo < s_fhi) ++s_flo;
   s_fhi -= (s_fhi - s_flo) & 1;
   int si = 0;
-  for (; si < s_flo; ++si) step(std::true_type{}, si & 1, t_lo + KS * si);
+  for (; si < s_flo; ++si) step(std::true_type{}, si & 1, t_lo + ks * si);
   for (; si < s_fhi; si += 2) {
-    step(std::false_type{}, std::integral_constant<int, 0>{}, t_lo + KS * si);
-    step(std::false_type{}, std::integral_constant<int, 1>{}, t_lo + KS * (si + 1));
+    step(std::false_type{}, std::integral_constant<int, 0>{}, t_lo + ks * si);
+    step(std::false_type{}, std::integral_constant<int, 1>{}, t_lo + ks * (si + 1));
   }
-  for (; si < s_hi; ++si) step(std::true_type{}, si & 1, t_lo + KS * si);
+  for (; si < s_hi; ++si) step(std::true_type{}, si & 1, t_lo + ks * si);
 
-  if constexpr (KS == 2) {
+  if (KS != 1 && ks == 2) {
     // Merge the two key halves of each row group: wavefront 2r+1 hands its
     // (m, l, O) to wavefront 2r through LDS (the K buffers are free once every
     // wavefront has passed the barrier).  Lane-for-lane: both hold the same
     // rows and head_dim columns.
     float* mo = (float*)lds_k0;  // [row group][DB*16][64 lanes]
     float* ml = (float*)lds_v0;  // [row group][2][64 lanes]
-    const int rg = wave / KS;
+    const int rg = wave / 2;
     __syncthreads();
     if (kp == 1) {
 #pragma unroll
@@ -767,12 +780,23 @@ hipError_t launch_feat_plain(const FwdParams& p, int feat, hipStream_t st) {
   return hipErrorNotSupported;
 }
 
+// Launcher of the per-item key split (KS = 0, D = 64): causal calls without
+// a mask, dropout or the fused q norm, with or without ALiBi.
+template <class E, int D>
+hipError_t launch_feat_split(const FwdParams& p, int feat, hipStream_t st) {
+  const dim3 grid((unsigned)p.total_work), block(4 * 64);
+  if (feat == 0) return launch_kernel(&attn_fwd_mfma16<E, D, 64, 4, 2, 0, false, false, false, false>, grid, block, 0, st, p);
+  if (feat == kFeatAlibi)
+    return launch_kernel(&attn_fwd_mfma16<E, D, 64, 4, 2, 0, true, false, false, false>, grid, block, 0, st, p);
+  return hipErrorNotSupported;
+}
+
 // Tile configs built per (dtype, D), every feature combination:
 // (nw, occ, bn, ks) = (4, 2, 64, 1) for D <= 128; (4, 1, 64, 1) for D = 256,
 // whose Q fragment (64 VGPRs) and O accumulator (128) need one wavefront per
 // SIMD, and whose double-buffered K/V tiles take 128 KiB of LDS; and for D = 64
 // also (4, 2, 64, 2), the key split for small grids (64 KiB of LDS: two
-// tiles per buffer).  For D = 128 without a mask or dropout also (8, 2, 128,
+// tiles per buffer), and (4, 2, 64, 0), the key split per work item.  For D = 128 without a mask or dropout also (8, 2, 128,
 // 1): 256 rows and 128-key tiles per workgroup (128 KiB of LDS, one
 // workgroup per CU).
 #define TRINIX_ATTN16_LAUNCHER(NAME, E, D)                                                                   \
@@ -783,8 +807,10 @@ hipError_t launch_feat_plain(const FwdParams& p, int feat, hipStream_t st) {
         return launch_feat_plain<E, D, 128, 8, 2, 1>(p, feat, st);                                         \
     if (cfg.bn != 64 || cfg.nw != 4 || cfg.occ != kOcc) return hipErrorNotSupported;                       \
     if (cfg.ks == 1) return launch_feat<E, D, 64, 4, kOcc, 1>(p, feat, st);                                \
-    if constexpr ((D) == 64)                                                                               \
+    if constexpr ((D) == 64) {                                                                             \
       if (cfg.ks == 2) return launch_feat<E, D, 64, 4, kOcc, 2>(p, feat, st);                              \
+      if (cfg.ks == 0) return launch_feat_split<E, D>(p, feat, st);                                        \
+    }                                                                                                      \
     return hipErrorNotSupported;                                                                             \
   }
 

@@ -3,6 +3,7 @@
 // status, a plan or a tile shape.
 #include "host_plan.h"
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 
@@ -69,10 +70,14 @@ static bool wide_grid(int64_t batch, int64_t hq, int64_t sq, bool banded) {
   const int64_t need = banded ? 2 * kSmallGrid : kSmallGrid;
   return batch * hq >= need || batch * hq * ((sq + 255) / 256) >= need;
 }
-Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain) {
+Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain,
+                 bool split_ok) {
   Cfg16 c{4, head_dim == 256 ? 1 : 2, 64, 1};
   // batch * hq * row blocks, without overflow (each factor < 2^31 here)
   if (head_dim == 64 && batch * hq <= kSmallGrid && batch * hq * ((sq + 127) / 128) <= kSmallGrid) c.ks = 2;
+  else if (head_dim == 64 && split_ok && batch * hq <= 2 * kSmallGrid &&
+           batch * hq * ((sq + 127) / 128) <= 2 * kSmallGrid)
+    c.ks = 0;
   if (head_dim == 128 && plain && wide_grid(batch, hq, sq, banded)) c = Cfg16{8, 2, 128, 1};
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
     int nw = 0, occ = 0, bn = 0, ks = 1;
@@ -80,6 +85,42 @@ Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool b
       c = Cfg16{nw, occ, bn, ks};
   }
   return c;
+}
+
+// Per-item key split for causal grids of up to two rounds of 128-row
+// workgroups at head_dim 64 (C2: 384): the longest row blocks' chains of
+// tiles set the kernel time there, so the longest blocks run as two 64-row
+// items with two wavefronts per 32-row group (half the chain each), the
+// others as one item.  Blocks are split longest first while the grid stays
+// within one round of resident workgroups (two per CU: 2 * 256 for all
+// (batch, q-head) pairs), since a workgroup of a second round pays its
+// start-up and epilogue again after the first round.
+int plan_split_rows(int64_t sq, int64_t sk, int64_t heads, int rows, int bn, uint8_t* items, int max) {
+  const int64_t nb = (sq + rows - 1) / rows;
+  if (nb <= 0 || nb > 63 || heads <= 0) return 0;  // row block in 6 bits
+  auto tiles = [&](int64_t rb) {
+    const int64_t keys = std::min(sk, (rb + 1) * rows);  // causal: row i sees keys j <= i
+    return (keys + bn - 1) / bn;
+  };
+  const int64_t max_t = tiles(nb - 1);
+  const int64_t budget = std::min<int64_t>(max, std::max<int64_t>(nb, 2 * kSmallGrid / heads));
+  struct Item { int64_t chain; int rb, split, half; };
+  Item list[2 * 64];
+  int n = 0;
+  int64_t count = nb;  // items so far: one per block, one more per split block
+  for (int64_t rb = nb - 1; rb >= 0; --rb) {
+    const int64_t t = tiles(rb);
+    if (2 * t > max_t + 1 && count + 1 <= budget) {
+      ++count;
+      for (int h = 0; h < 2; ++h) list[n++] = Item{(t + 1) / 2, (int)rb, 1, h};
+    } else {
+      list[n++] = Item{t, (int)rb, 0, 0};
+    }
+  }
+  if (n > max) return 0;
+  std::stable_sort(list, list + n, [](const Item& a, const Item& b) { return a.chain > b.chain; });
+  for (int k = 0; k < n; ++k) items[k] = (uint8_t)((list[k].rb << 2) | (list[k].split << 1) | list[k].half);
+  return n;
 }
 
 // The dQ backward kernel takes the same wide shape (8 wavefronts x 32 rows,

@@ -13,8 +13,12 @@ struct Cfg16 {
   int nw;   // wavefronts per workgroup (32 query rows per key split)
   int occ;  // target wavefronts per SIMD (register budget 512 / occ)
   int bn;   // keys per K/V tile
-  int ks;   // key split: wavefronts sharing one 32-row group (rows per workgroup = 32 * nw / ks)
+  int ks;   // key split: wavefronts sharing one 32-row group (rows per workgroup = 32 * nw / ks);
+            // 0: per work item, from plan_split_rows
 };
+
+// Work items of the per-item key split, at most kMaxRowItems per (batch, q-head).
+constexpr int kMaxRowItems = 128;
 
 // Largest 16-bit K/V key-row stride (elements) the forward's 32-bit in-tile
 // offsets address: 128 rows * 2 B * 2^22 = 2^30 bytes.
@@ -26,8 +30,19 @@ int validate_fwd_args(const trinix_attn_fwd_args* a);
 int validate_bwd_args(const trinix_attn_bwd_args* a);
 
 // Tile configuration of the 16-bit forward for a problem: `banded` when
-// causal or windowed, `plain` without a mask or dropout.
-Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain);
+// causal or windowed, `plain` without a mask or dropout, `split_ok` when the
+// per-item key split applies (causal, no window, no mask, dropout or fused
+// q norm).
+Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool plain,
+                 bool split_ok = false);
+// Work items of the per-item key split for a causal problem of `heads`
+// (batch * q-heads) row sequences, row blocks of `rows` (= 32 * nw) rows and
+// `bn`-key tiles: the longest row blocks (tile count above half the longest)
+// run as two items (split, half 0 / 1) while the grid keeps one round of
+// resident workgroups, the rest as one; items ordered by chain length (tiles
+// per wavefront), longest first.  Writes `items` and returns their count, or
+// 0 if more than `max`.
+int plan_split_rows(int64_t sq, int64_t sk, int64_t heads, int rows, int bn, uint8_t* items, int max);
 // Whether the 16-bit dQ backward runs 256-row workgroups with 128-key tiles.
 bool pick_dq_wide(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool masked);
 
