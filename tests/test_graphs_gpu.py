@@ -1,5 +1,5 @@
 """HIP graph capture of the attention paths (serving loops capture decode
-steps).  Every entry point enqueues its kernels on the caller's stream and
+steps; training loops capture whole steps, backward included).  Every entry point enqueues its kernels on the caller's stream and
 allocates nothing itself; the host layer's only device-to-host read (the
 position_ids range check) is skipped while a stream is capturing, and the
 kernels clamp ids to the tables instead.
@@ -116,3 +116,37 @@ def test_graph_layer_decode_step_with_cache_rope_and_qk_norm():
 
     g, outs = capture(fn)
     replay_and_check(g, outs, [x, past_k, past_v], fn)
+
+
+def test_graph_forward_backward():
+    """A training step's attention (forward and backward to q, k, v through
+    the MFMA backward kernels) captured whole, as PyTorch's whole-network
+    capture does: every replay's gradients equal an eager step's."""
+    B, S, H, HKV, D = 1, 320, 4, 2, 128
+    dt = torch.bfloat16
+    q = torch.zeros(B, S, H, D, device=DEV, dtype=dt, requires_grad=True)
+    k = torch.zeros(B, S, HKV, D, device=DEV, dtype=dt, requires_grad=True)
+    v = torch.zeros(B, S, HKV, D, device=DEV, dtype=dt, requires_grad=True)
+    dout = torch.zeros(B, S, H, D, device=DEV, dtype=dt)
+
+    def fn():
+        q.grad = k.grad = v.grad = None
+        out = triton_attn_func(q, k, v, causal=True)
+        out.backward(dout)
+        return out.detach(), q.grad, k.grad, v.grad
+
+    g, static = capture(fn)
+    for rnd in range(3):
+        gen = torch.Generator(device=DEV).manual_seed(2000 + rnd)
+        with torch.no_grad():
+            for t in (q, k, v, dout):
+                t.copy_(torch.randn(t.shape, device=DEV, generator=gen).to(dt))
+        torch.cuda.synchronize()
+        g.replay()
+        _ = torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)  # eager work between replays
+        torch.cuda.synchronize()
+        replayed = [t.clone() for t in static]
+        ref = fn()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "dq", "dk", "dv"), replayed, ref):
+            assert torch.equal(a, b), f"replay {rnd}: {name} differs from eager"
