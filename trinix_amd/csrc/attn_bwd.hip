@@ -56,7 +56,7 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   const int vrc = validate_bwd_args(a);
   if (vrc != TRINIX_OK) return vrc;
 
-  BwdParams p;
+  BwdParams p{};
   p.q = (const uint16_t*)a->q;
   p.k = (const uint16_t*)a->k;
   p.v = (const uint16_t*)a->v;

@@ -323,7 +323,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   const int vrc = validate_fwd_args(a);
   if (vrc != TRINIX_OK) return vrc;
 
-  FwdParams p;
+  FwdParams p{};  // value-initialised: fields a configuration does not use are zero
   p.q = (const uint16_t*)a->q;
   p.k = (const uint16_t*)a->k;
   p.v = (const uint16_t*)a->v;
