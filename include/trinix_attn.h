@@ -115,7 +115,7 @@ typedef struct trinix_attn_fwd_args {
   int64_t alibi_stride[2];
   const void* mask;             /* additive mask, NULL = none */
   int32_t mask_dtype;           /* trinix_dtype */
-  int64_t mask_stride[4];       /* b, h, i, j (0 = broadcast) */
+  int64_t mask_stride[4];       /* b, h, i, j (0 = broadcast); 0 <= (seqlen_k-1)*j < 2^31 */
   const uint8_t* mask_blockmap; /* from trinix_attn_mask_blockmap, or NULL */
   int64_t blockmap_stride[2];   /* b, h strides of the block map (0 = broadcast) */
   float dropout_p;              /* 0 <= p < 1 */
@@ -317,7 +317,7 @@ typedef struct trinix_attn_bwd_args {
   int64_t alibi_stride[2];
   const void* mask;
   int32_t mask_dtype;
-  int64_t mask_stride[4];
+  int64_t mask_stride[4];      /* as in trinix_attn_fwd_args */
   const uint8_t* mask_blockmap;
   int64_t blockmap_stride[2];
   float dropout_p;              /* the forward's dropout_p, seed and offset */

@@ -43,7 +43,9 @@
 namespace trinix {
 
 template <class E, int D, int BN, int NW, int OCC, int KS, bool ALIBI, bool MASK, bool DROP, bool QN>
-__global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams p) {
+// The head_dim 64 mask kernels are held to three wavefronts per SIMD (168
+// VGPRs); the other shapes to OCC.
+__global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd_mfma16(const FwdParams p) {
   // KS = 2 splits each 32-row group's keys between two wavefronts: wavefront
   // 2r + kp owns rows 32r..32r+31 and the tiles t_lo + KS*s + kp; the halves
   // merge through LDS at the end.  It halves the longest dependency chain of
@@ -398,7 +400,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
   constexpr int NQK = NB * DS;
   // mask kernels (and D = 256, with 192 registers of Q and O) hold more live
   // values: shorter read-ahead
-  constexpr int KPF = D == 256 ? (MASK ? 1 : 2) : (MASK && D > 64 ? (DROP ? 2 : 3) : 6);
+  constexpr int KPF = D == 256 ? (MASK ? 1 : 2) : (MASK ? (DROP ? 2 : 3) : 6);
   // Byte offset of K fragment (nb, ds) of this lane in a K tile: row
   // nb*32 + r, unit (2ds + g) ^ swz_k(r) (the swizzle depends only on r).  As
   // 16*((2ds) ^ (g ^ swz)) = 32*ds ^ 16*(g ^ swz) and the row offset has no
@@ -461,7 +463,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
     return (u32x4_t){l2[0], l2[1], h2[0], h2[1]};
   };
   constexpr int NPV = DB * NB * 2;
-  constexpr int VPF = D == 256 ? (MASK ? 1 : 2) : (MASK && D > 64 ? (DROP ? 1 : 2) : 4);
+  constexpr int VPF = D == 256 ? (MASK ? 1 : 2) : (MASK ? (DROP ? 1 : 2) : 4);
   // vpre: the first VPF fragments, read ahead (before the softmax) by the caller.
   auto pv = [&](const uint16_t* vt, const u32x4_t(&pb)[NB][2], const u32x4_t(&vpre)[VPF]) __attribute__((always_inline)) {
     u32x4_t vf[NPV];
@@ -503,10 +505,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void attn_fwd_mfma16(const FwdParams 
             load_mask4(mrow, p.mask_dtype, n0 + nb * 32 + vq * 8 + g * 4, p.mk_sj, p.Sk - 1, mv);
 #pragma unroll
             for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = __builtin_fmaf(mv[e], mscale, s[nb][vq * 4 + e]);
-            // D = 256 (every register in use) or with dropout: one group of
-            // mask values in flight at a time, or their loads are hoisted
-            // together and the kernel spills
-            if constexpr (D == 256 || DROP) __builtin_amdgcn_sched_barrier(0);
+            // D = 256 (every register in use), D = 64 (held to 168 VGPRs)
+            // or with dropout: one group of mask values in flight at a time,
+            // or their loads are hoisted together and the kernel spills
+            if constexpr (D == 256 || D == 64 || DROP) __builtin_amdgcn_sched_barrier(0);
           }
       }
     }

@@ -56,11 +56,13 @@ __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx)
 
 // Mask values of keys j0..j0+3 (element stride sj) of one row: one
 // wave-uniform dtype switch for the four loads, keys past jmax read key jmax
-// (their scores are masked anyway), so the loads carry no branches.
+// (their scores are masked anyway), so the loads carry no branches.  The
+// element offsets within a row are 32-bit: the host requires
+// 0 <= (Sk - 1) * sj < 2^31 (check_mask_stride).
 __device__ inline void load_mask4(const void* base, int dtype, int j0, int64_t sj, int jmax, float (&mv)[4]) {
-  int64_t idx[4];
+  uint32_t idx[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) idx[e] = (int64_t)min(j0 + e, jmax) * sj;
+  for (int e = 0; e < 4; ++e) idx[e] = (uint32_t)min(j0 + e, jmax) * (uint32_t)sj;
   switch (dtype) {
     case TRINIX_F32:
 #pragma unroll

@@ -138,6 +138,12 @@ bool pick_dq_wide(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool 
   return wide_grid(batch, hq, sq, banded);
 }
 
+// The kernels address a mask row with 32-bit element offsets (load_mask4):
+// a key stride in [0, 2^31 / Sk).  A mask broadcast over keys has stride 0.
+static bool mask_key_stride_ok(int64_t sj, int64_t sk) {
+  return sj >= 0 && (sk <= 1 || sj <= ((1ll << 31) - 1) / (sk - 1));  // (sk - 1) * sj < 2^31, no overflow
+}
+
 int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (!a) return TRINIX_ERR_NULL_POINTER;
   const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
@@ -162,6 +168,7 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
       a->mask_dtype != TRINIX_U8)
     return TRINIX_ERR_BAD_DTYPE;
   if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->mask && !mask_key_stride_ok(a->mask_stride[3], a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
   if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
   if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
   if (a->rope_cos && esize == 2 &&
@@ -198,6 +205,7 @@ int validate_bwd_args(const trinix_attn_bwd_args* a) {
       a->mask_dtype != TRINIX_U8)
     return TRINIX_ERR_BAD_DTYPE;
   if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->mask && !mask_key_stride_ok(a->mask_stride[3], a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
   return TRINIX_OK;
 }
 
