@@ -199,7 +199,11 @@ def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0):
     return (time.perf_counter() - t0) * 1e3 / iters
 
 
-def measure(w, args, torch, cold=False):
+def measure(w, args, torch, cold=False, min_timed_s=0.0):
+    """(inputs, flop, step ms, graph kernel ms, cold-MALL ms, steps timed).
+    The step loop times ``args.steps`` steps, or more when ``min_timed_s``
+    asks for a longer timed region (the extra workloads of ``--all``: at
+    C2's 16 us per step, 20 steps would be mostly the final synchronize)."""
     from trinix_amd.workloads import make_inputs, flops
 
     inp = make_inputs(w, device="cuda")
@@ -214,17 +218,21 @@ def measure(w, args, torch, cold=False):
         if n % 8 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
+    steps = args.steps
+    if min_timed_s > 0.0:
+        per_step_s = (time.perf_counter() - t_warm) / n
+        steps = max(steps, int(min_timed_s / per_step_s) + 1)
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         fn()
     torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms = (time.perf_counter() - t0) * 1e3 / steps
     fl = flops(w)
     # kernel time from a HIP graph of back-to-back calls (every workload:
     # at C2's size an event-timed Python loop measures the host)
     kms = graph_ms(kernel_only_fn(w, inp, torch), torch)
     cold_ms = cold_step_ms(fn, torch) if cold else None
-    return inp, fl, ms, kms, cold_ms
+    return inp, fl, ms, kms, cold_ms, steps
 
 
 DECODE = dict(batch=16, seqlen_k=8192, nheads_q=32, nheads_kv=8, head_dim=128)
@@ -413,7 +421,7 @@ def main():
 
     w = WORKLOADS[args.workload]
     dname = DTYPE_NAME[str(w.dtype)]
-    inp, fl, ms, kms, cold_ms = measure(w, args, torch, cold=not args.no_extra)
+    inp, fl, ms, kms, cold_ms, _ = measure(w, args, torch, cold=not args.no_extra)
     value = fl / (ms * 1e-3) / 1e12
     k_tflops = fl / (kms * 1e-3) / 1e12
     peak = PEAK_TFLOPS[dname]
@@ -482,9 +490,9 @@ def main():
                 continue
             # kernel_ms from a graph of back-to-back calls: several of these
             # shapes run for less time than one call's host work
-            _, f2, ms2, kms2, _ = measure(wo, args, torch)
+            _, f2, ms2, kms2, _, n2 = measure(wo, args, torch, min_timed_s=0.05)
             pk = PEAK_TFLOPS[DTYPE_NAME[str(wo.dtype)]]
-            extra[name] = {"ms": round(ms2, 4), "tflops": round(f2 / ms2 / 1e9, 2),
+            extra[name] = {"ms": round(ms2, 4), "steps": n2, "tflops": round(f2 / ms2 / 1e9, 2),
                            "kernel_ms": round(kms2, 4), "kernel_tflops": round(f2 / kms2 / 1e9, 2),
                            "pct_of_peak": round(100 * f2 / ms2 / 1e9 / pk, 2),
                            "kernel_pct_of_peak": round(100 * f2 / kms2 / 1e9 / pk, 2)}
