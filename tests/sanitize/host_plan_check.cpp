@@ -158,6 +158,29 @@ int main() {
     CHECK(validate_bwd_args(&a) == TRINIX_ERR_BAD_STRIDE, "bwd stride");
     cases += 5;
   }
+  // ---- the tuning override TRINIX_ATTN_CFG="nw,occ,bn[,ks]": ks 0 (the
+  // per-item split), 1 and 2 are taken, anything else leaves the planner's
+  // choice
+  {
+    auto forced = [](const char* v) {
+      setenv("TRINIX_ATTN_CFG", v, 1);
+      const Cfg16 c = pick_cfg16(64, 1, 4, 512, true, true, true);
+      unsetenv("TRINIX_ATTN_CFG");
+      return c;
+    };
+    const Cfg16 dflt = pick_cfg16(64, 1, 4, 512, true, true, true);
+    Cfg16 c = forced("4,2,64,0");
+    CHECK(c.nw == 4 && c.occ == 2 && c.bn == 64 && c.ks == 0, "override ks 0");
+    c = forced("4,2,64,2");
+    CHECK(c.ks == 2, "override ks 2");
+    c = forced("8,2,128");
+    CHECK(c.nw == 8 && c.bn == 128 && c.ks == 1, "override without ks");
+    c = forced("4,2,64,3");
+    CHECK(c.nw == dflt.nw && c.bn == dflt.bn && c.ks == dflt.ks, "override ks 3 rejected");
+    c = forced("3,2,64,2");
+    CHECK(c.nw == dflt.nw && c.ks == dflt.ks, "override nw not a multiple of ks rejected");
+    cases += 5;
+  }
   // ---- fuzz: every field over its whole range
   int accepted = 0, planned = 0;
   for (int it = 0; it < 200000; ++it) {

@@ -81,7 +81,9 @@ Cfg16 pick_cfg16(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool b
   if (head_dim == 128 && plain && wide_grid(batch, hq, sq, banded)) c = Cfg16{8, 2, 128, 1};
   if (const char* env = getenv("TRINIX_ATTN_CFG")) {
     int nw = 0, occ = 0, bn = 0, ks = 1;
-    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &ks) >= 3 && nw > 0 && ks > 0 && nw % ks == 0)
+    // ks 1 or 2: wavefronts per 32-row group; 0: the per-item split
+    if (sscanf(env, "%d,%d,%d,%d", &nw, &occ, &bn, &ks) >= 3 && nw > 0 && ks >= 0 && ks <= 2 &&
+        (ks == 0 || nw % ks == 0))
       c = Cfg16{nw, occ, bn, ks};
   }
   return c;
