@@ -206,6 +206,50 @@ def test_gqa_equals_repeated_kv_bitwise():
     assert torch.equal(out_g, out_r)
 
 
+LONG_CASES = [
+    # (S, H, Hkv, D, dtype, causal, window): one sequence, S query rows and keys
+    (65536, 2, 1, 128, torch.bfloat16, True, None),        # 1024 key tiles in the last rows' chain
+    (131072, 1, 1, 64, torch.float16, True, (8192, 0)),    # 2^17 rows, a window of 8192 keys
+    (98304, 4, 4, 128, torch.bfloat16, False, (1000, 300)),  # two-sided window, K/V rows of 1 KiB
+]
+
+
+@pytest.mark.parametrize("case", LONG_CASES, ids=[f"S{c[0]}-D{c[3]}" for c in LONG_CASES])
+def test_long_context_row_bands(case):
+    """Sequences of 64K-128K positions: output and lse against the oracle on
+    the first, a middle and the last 64-row band (their key ranges hold
+    every key the causal / window band lets them see), so the 64-bit tile
+    base addresses, the longest causal chains and the window arithmetic are
+    exercised at lengths no BASELINE workload reaches."""
+    S, H, Hkv, D, dtype, causal, window = case
+    q, k, v = rand((1, S, H, D), dtype, 131), rand((1, S, Hkv, D), dtype, 132), rand((1, S, Hkv, D), dtype, 133)
+    out, lse = TritonAttentionKernel.apply(q, k, v, causal=causal, window_size=window, return_lse=True)
+    out, lse = out.cpu(), lse.cpu()
+    qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+    band = 64
+    for r0 in (0, S // 2 - 37, S - band):
+        lo = 0 if window is None else max(0, r0 - window[0])
+        hi = r0 + band if causal else (S if window is None else min(S, r0 + band + window[1]))
+        ref = orc.functional_attention(qc, kc, vc, causal=causal, window_size=window, rows=(r0, r0 + band),
+                                       keys=(lo, hi), head_chunk=H)
+        assert_parity(out[:, r0:r0 + band], ref, dtype, f"S={S} rows {r0}..{r0 + band - 1}")
+        # lse of the band in fp64 from the same rows and keys
+        qs = qc[0, r0:r0 + band].double().transpose(0, 1)                      # (H, band, D)
+        ks = kc[0, lo:hi].double().repeat_interleave(H // Hkv, dim=1).transpose(0, 1)  # (H, keys, D)
+        s = qs @ ks.transpose(1, 2) * D ** -0.5
+        i = torch.arange(r0, r0 + band)[:, None]
+        j = torch.arange(lo, hi)[None, :]
+        allowed = torch.ones_like(s[0], dtype=torch.bool)
+        if causal:
+            allowed &= j <= i
+        if window is not None:
+            allowed &= (j - i >= -window[0]) & (j - i <= window[1])
+        s = s.masked_fill(~allowed, float("-inf"))
+        ref_lse = torch.logsumexp(s, dim=-1)
+        d = (lse[0, :, r0:r0 + band].double() - ref_lse).abs().max().item()
+        assert d <= 2e-2, f"S={S} rows {r0}..: lse err {d:.3g}"
+
+
 def test_mqa_stride0_equals_materialised_bitwise():
     w = WORKLOADS["c5b"]
     inp = make_inputs(w)
