@@ -67,6 +67,8 @@ CASES = [
     (2, 5, 5000, 3, 1, 64, "many"),     # G=3: 15 packed rows
     (160, 1, 256, 8, 8, 128, 1),        # >= 1024 work items: one chunk, direct output
     (1, 1, 1, 4, 4, 128, 1),            # a single key
+    (1, 1, 131072, 32, 8, 128, "many"),  # a 128K-token cache (long context)
+    (2, 3, 100000, 8, 1, 64, "many"),    # MQA over 100K keys, ragged last chunk
 ]
 
 
