@@ -457,3 +457,39 @@ def test_backward_full_size_against_fp32_eager(wl):
         d = (h - t).abs()
         assert d.max().item() <= 1e-2 * t.abs().max().item(), (name, d.max().item(), t.abs().max().item())
         assert d.mean().item() <= 6e-3 * t.abs().mean().item(), (name, d.mean().item(), t.abs().mean().item())
+
+
+LONG_BWD_CASES = [
+    # (S, H, Hkv, D, dtype, window, r0): dO nonzero on rows r0..r0+63 only
+    (32768, 2, 1, 128, torch.bfloat16, None, 32768 - 64),      # the longest causal chain (512 key tiles)
+    (65536, 1, 1, 64, torch.float16, (4096, 0), 40000),        # a causal window inside a 64K sequence
+]
+
+
+@pytest.mark.parametrize("case", LONG_BWD_CASES, ids=[f"S{c[0]}-D{c[3]}" for c in LONG_BWD_CASES])
+def test_backward_long_context_one_row_band(case):
+    """Gradients of a 32K / 64K-position causal call whose dO is zero outside
+    one 64-row band: dQ is then zero outside the band (dP = dO V^T = 0 and
+    delta = rowsum(dO O) = 0 there), and dK / dV are the band's contribution
+    alone, so the whole of every gradient has an exact reference from the
+    band's rows: fp64 and bf16/fp16 autograd of the oracle on those rows
+    (the usual bar)."""
+    S, H, Hkv, D, dtype, window, r0 = case
+    print(f"long backward S={S} D={D}", flush=True)
+    q, k, v, _ = _inputs(1, S, S, H, Hkv, D, seed=140)
+    do = torch.zeros(1, S, H, D)
+    do[:, r0:r0 + 64] = torch.randn(1, 64, H, D, generator=torch.Generator().manual_seed(141))
+    kw = dict(causal=True, window_size=window)
+    lo = 0 if window is None else max(0, r0 - window[0])
+    band = dict(kw, rows=(r0, r0 + 64), keys=(lo, r0 + 64), head_chunk=H)
+
+    def band_grads(dt):
+        ts = [t.detach().to(dt).clone().requires_grad_(True) for t in (q, k, v)]
+        orc.functional_attention(*ts, **band).backward(do[:, r0:r0 + 64].to(dt))
+        return [t.grad.double() for t in ts]
+
+    truth, eager = band_grads(torch.float64), band_grads(dtype)
+    _, hip = _hip_grads(q, k, v, do, dtype, **kw)
+    for t in (hip[0][:, :r0], hip[0][:, r0 + 64:], hip[1][:, r0 + 64:], hip[2][:, r0 + 64:], hip[2][:, :lo]):
+        assert int(torch.count_nonzero(t)) == 0  # outside the band's rows / keys: exactly zero
+    _check(hip, eager, truth)
