@@ -64,6 +64,10 @@ CASES = [
     (1, 17, 17, 1, 1, 128, torch.float16, dict(causal=True)),
     (1, 40, 70, 2, 1, 64, torch.bfloat16, dict()),
     (2, 64, 200, 3, 1, 128, torch.bfloat16, dict(window_size=(0, 90))),
+    # top-left causal with Sq != Sk: keys past Sq - 1 get no gradient (Sq < Sk);
+    # rows past Sk - 1 see every key (Sq > Sk)
+    (1, 100, 180, 2, 1, 128, torch.bfloat16, dict(causal=True)),
+    (1, 180, 100, 2, 2, 64, torch.float16, dict(causal=True)),
 ]
 
 
