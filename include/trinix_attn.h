@@ -118,6 +118,11 @@ typedef struct trinix_attn_fwd_args {
   int64_t mask_stride[4];       /* b, h, i, j (0 = broadcast); 0 <= (seqlen_k-1)*j < 2^31 */
   const uint8_t* mask_blockmap; /* from trinix_attn_mask_blockmap, or NULL */
   int64_t blockmap_stride[2];   /* b, h strides of the block map (0 = broadcast) */
+  /* Dropout on the attention weights: key j of row i of (b, h) is dropped
+   * when 16-bit field j % 8 (word (j % 8) / 2, low half for even j) of
+   * Philox4x32-10(counter (j / 8, i, b*H + h, offset_lo), key (seed_lo ^
+   * offset_hi, seed_hi)) is below floor(p * 2^16); kept weights are scaled
+   * by 1 / (1 - p). */
   float dropout_p;              /* 0 <= p < 1 */
   uint64_t dropout_seed;
   uint64_t dropout_offset;

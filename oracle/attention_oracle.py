@@ -431,10 +431,14 @@ def philox4x32_10(ctr: np.ndarray, key: Tuple[int, int]) -> np.ndarray:
 def dropout_keep(batch: int, nheads: int, seqlen_q: int, seqlen_k: int, p: float, seed: int,
                  offset: int = 0) -> np.ndarray:
     """Keep mask (B,H,Sq,Sk) of the kernel's dropout: for key j of row i of
-    (b, h), counter (j >> 2, i, b*H + h, offset_lo), key (seed_lo ^
-    offset_hi, seed_hi), word j & 3; dropped iff word < floor(p * 2^32)."""
-    thresh = min(int(p * 4294967296.0), 0xFFFFFFFF)
-    ngrp = -(-seqlen_k // 4)
+    (b, h), the Philox call with counter (j >> 3, i, b*H + h, offset_lo) and
+    key (seed_lo ^ offset_hi, seed_hi) gives four words; key j takes 16-bit
+    field j & 7 of them (word (j & 7) >> 1, the low half for even j) and is
+    dropped iff that field < floor(p * 2^16) (kernels: csrc/common.h
+    keep_field, dropout_pair in attn_params.h, keep_bits_of_key in
+    attn_bwd16.h)."""
+    thresh = min(int(p * 65536.0), 65535)
+    ngrp = -(-seqlen_k // 8)
     bh = np.arange(batch * nheads, dtype=np.uint32)[:, None, None]
     ii = np.arange(seqlen_q, dtype=np.uint32)[None, :, None]
     gg = np.arange(ngrp, dtype=np.uint32)[None, None, :]
@@ -442,5 +446,7 @@ def dropout_keep(batch: int, nheads: int, seqlen_q: int, seqlen_k: int, p: float
     ctr = np.stack([np.broadcast_to(gg, shape), np.broadcast_to(ii, shape), np.broadcast_to(bh, shape),
                     np.full(shape, offset & 0xFFFFFFFF, dtype=np.uint32)], axis=-1)
     key = ((seed & 0xFFFFFFFF) ^ ((offset >> 32) & 0xFFFFFFFF), (seed >> 32) & 0xFFFFFFFF)
-    words = philox4x32_10(ctr, key).reshape(batch * nheads, seqlen_q, ngrp * 4)[:, :, :seqlen_k]
-    return (words >= np.uint32(thresh)).reshape(batch, nheads, seqlen_q, seqlen_k)
+    words = philox4x32_10(ctr, key)  # (BH, Sq, ngrp, 4)
+    fields = np.stack([words & np.uint32(0xFFFF), words >> np.uint32(16)], axis=-1)  # field k = word k>>1, half k&1
+    fields = fields.reshape(batch * nheads, seqlen_q, ngrp * 8)[:, :, :seqlen_k]
+    return (fields >= np.uint32(thresh)).reshape(batch, nheads, seqlen_q, seqlen_k)

@@ -302,6 +302,12 @@ DROP_CASES = [
     (1, 150, 150, 2, 1, 128, torch.bfloat16, 0.1, dict(attn_mask=_drop_mask(150, 150, 32), causal=True)),
     (1, 17, 17, 1, 1, 128, torch.float16, 0.1, dict(causal=True)),
     (1, 40, 70, 2, 1, 64, torch.bfloat16, 0.05, dict(softmax_scale=0.2)),
+    # ALiBi + mask + dropout at head_dim 128: the dQ variant whose lanes make
+    # their own Philox calls (no lane-pair exchange; every register in use)
+    (1, 140, 140, 4, 2, 128, torch.float16, 0.2, dict(alibi_slopes=orc.alibi_slopes(4),
+                                                      attn_mask=_drop_mask(140, 140, 33), causal=True)),
+    (2, 70, 90, 2, 2, 128, torch.bfloat16, 0.35, dict(alibi_slopes=orc.alibi_slopes(2),
+                                                      attn_mask=_drop_mask(70, 90, 34))),
 ]
 
 

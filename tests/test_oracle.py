@@ -193,6 +193,28 @@ def test_dropout_keep_statistics():
     assert np.array_equal(keep, orc.dropout_keep(2, 3, 64, 100, 0.25, seed=77))
 
 
+def test_dropout_keep_field_mapping():
+    """Key j of row i takes 16-bit field j % 8 of the four Philox words of
+    counter (j // 8, i, b*H + h, offset_lo): at p = 0.5 the keep test
+    (field >= 2^15) is the field's top bit, so the mask must equal bit
+    16*(j % 2) + 15 of word (j % 8) // 2, read off single scalar calls; at
+    p = 1 - 2^-16 only fields equal to 0xFFFF are kept."""
+    B, H, Sq, Sk, seed, off = 1, 2, 5, 21, 0x1234_5678_9ABC, (7 << 32) | 3
+    keep = orc.dropout_keep(B, H, Sq, Sk, 0.5, seed, off)
+    key = ((seed & 0xFFFFFFFF) ^ (off >> 32), seed >> 32)
+    for h in range(H):
+        for i in range(Sq):
+            for j in range(Sk):
+                w = orc.philox4x32_10(np.array([j // 8, i, h, off & 0xFFFFFFFF], dtype=np.uint32), key)
+                bit = (int(w[(j % 8) // 2]) >> (16 * (j % 2) + 15)) & 1
+                assert bool(keep[0, h, i, j]) == bool(bit), (h, i, j)
+    keep_hi = orc.dropout_keep(B, H, Sq, Sk, 1.0 - 2.0 ** -16, seed, off)
+    w = orc.philox4x32_10(np.array([[[0, i, h, off & 0xFFFFFFFF] for i in range(Sq)] for h in range(H)],
+                                   dtype=np.uint32), key)
+    fields = np.stack([w & 0xFFFF, w >> 16], axis=-1).reshape(H, Sq, 8)
+    assert np.array_equal(keep_hi[0, :, :, :8], fields == 0xFFFF)
+
+
 def test_dropout_in_eager_restatement_pinned():
     """Dropout with a given keep mask (base.py:395): against the fp64
     closed form, and two cases the mathematics fixes: a mask keeping

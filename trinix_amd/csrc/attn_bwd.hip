@@ -105,8 +105,9 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
     return TRINIX_ERR_BAD_SHAPE;
   p.use_dropout = a->dropout_p > 0.f ? 1 : 0;
   {
-    const double th = (double)a->dropout_p * 4294967296.0;
-    p.drop_thresh = th >= 4294967295.0 ? 0xffffffffu : (uint32_t)th;
+    // dropped when the key's 16-bit Philox field < floor(p * 2^16)
+    const double th = (double)a->dropout_p * 65536.0;
+    p.drop_thresh = th >= 65535.0 ? 65535u : (uint32_t)th;
     p.drop_scale = a->dropout_p > 0.f ? 1.f / (1.f - a->dropout_p) : 1.f;
   }
   p.seed_lo = (uint32_t)a->dropout_seed;

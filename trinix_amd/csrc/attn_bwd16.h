@@ -24,6 +24,7 @@
 // dZ = P (dP - delta) from the rounded P (bwd_dq from the fp32 one).
 #pragma once
 #include <climits>
+#include <utility>
 
 #include "attn_params.h"
 #include "lds_tile.h"
@@ -58,9 +59,9 @@ struct BwdParams {
   int bm_cols;
   int num_kblk, num_mblk;  // 128-key blocks (dK/dV), 128- or 256-row blocks (dQ)
   int dq_wide;             // dQ in 256-row workgroups with 128-key tiles
-  // dropout of the forward (attn_params.h dropout_group): same Philox stream
+  // dropout of the forward (common.h keep_field): same Philox stream
   int use_dropout;
-  uint32_t drop_thresh;  // dropped when the Philox word < drop_thresh
+  uint32_t drop_thresh;  // dropped when the 16-bit Philox field < drop_thresh
   float drop_scale;      // 1 / (1 - p)
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
 };
@@ -138,35 +139,47 @@ struct TileReader {
   }
 };
 
-// Dropout of the forward (attn_params.h dropout_group), regenerated: (row i,
-// key j) is dropped when word j%4 of Philox(counter (j/4, i, b*Hq+h, off_lo),
-// key (seed_lo ^ off_hi, seed_hi)) is below drop_thresh.
+// Dropout of the forward (common.h keep_field), regenerated: (row i, key j)
+// is kept when 16-bit field j%8 of Philox(counter (j/8, i, b*Hq+h, off_lo),
+// key (seed_lo ^ off_hi, seed_hi)) is at least drop_thresh.
 //
-// keep_bits_of_key: for a lane that owns key j (j % 4 == lane % 4, the four
-// lanes of a quad holding keys 4m..4m+3) and the 16 query rows
-// r0 + (v>>2)*8 + (v&3), v = 0..15, bit v of the result is set when (row v,
-// j) is kept.  The forward draws one Philox call per (row, 4 consecutive
-// keys), so the lanes of a quad share every call: lane e makes the calls of
-// the rows with v&3 == e and the quad swaps the results through DPP quad
-// broadcasts (one call per 4 elements, as in the forward).
+// Lane q's value (q = 0..7 of each aligned 8-lane group) in every lane of
+// the group: a quad broadcast of lane q % 4 (quad_perm [q,q,q,q] = q * 0x55)
+// is right in q's own quad; the other quad takes it shifted by 4 lanes
+// (row_shr:4 = 0x114 into banks 1 and 3 when q < 4, row_shl:4 = 0x104 into
+// banks 0 and 2 when q >= 4).  DPP controls must be constants: q is a
+// template argument.
+template <int Q>
+__device__ inline uint32_t bcast8(uint32_t x) {
+  const int t = __builtin_amdgcn_mov_dpp((int)x, (Q & 3) * 0x55, 0xf, 0xf, false);
+  return (uint32_t)__builtin_amdgcn_update_dpp(t, t, Q < 4 ? 0x114 : 0x104, 0xf, Q < 4 ? 0xa : 0x5, false);
+}
+// Bits e8 and 8 + e8 of lane q's `own`, q = 0..7, at result bits q and q + 8.
+template <int... Q>
+__device__ inline uint32_t gather_keep_bits(uint32_t own, int e8, std::integer_sequence<int, Q...>) {
+  return ((((bcast8<Q>(own) >> e8) & 0x101u) << Q) | ...);
+}
+
+// keep_bits_of_key: for a lane that owns key j (lanes 8m'..8m'+7 of each
+// half-wave hold 8 consecutive keys, 8-aligned; e8 = j % 8) and the 16 query
+// rows r(v) = r0 + (v>>2)*8 + (v&3), v = 0..15, bit v of the result is set
+// when (row r(v), j) is kept.  The forward draws one Philox call per (row, 8
+// consecutive keys), so the eight lanes share every call: lane e8 makes the
+// calls of rows v = e8 and e8 + 8 (one call per 8 elements, as in the
+// forward) and the group hands out the keep bytes through DPP (bcast8).
 __device__ inline uint32_t keep_bits_of_key(const BwdParams& p, int bh, int j, int r0) {
-  const int e = j & 3;
-  uint32_t own = 0;  // bit vq*4 + k: row r0 + vq*8 + e, key 4*(j/4) + k
+  const int e8 = j & 7;
+  uint32_t own = 0;  // bit 8h + k: row r(e8 + 8h), key 8*(j/8) + k
 #pragma unroll
-  for (int vq = 0; vq < 4; ++vq) {
-    const u32x4_t c = {(uint32_t)(j >> 2), (uint32_t)(r0 + vq * 8 + e), (uint32_t)bh, p.off_lo};
+  for (int h = 0; h < 2; ++h) {
+    const int v = e8 + 8 * h;
+    const u32x4_t c = {(uint32_t)(j >> 3), (uint32_t)(r0 + (v >> 2) * 8 + (v & 3)), (uint32_t)bh, p.off_lo};
     const u32x4_t w = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) own |= (w[k] >= p.drop_thresh ? 1u : 0u) << (vq * 4 + k);
+    for (int k = 0; k < 8; ++k) own |= (keep_field(w[k >> 1], k & 1, p.drop_thresh) ? 1u : 0u) << (8 * h + k);
   }
-  // row v = vq*4 + q of this lane: bit vq*4 + e of quad lane q's `own`
-  // (DPP quad_perm [q,q,q,q] = q * 0x55)
-  const uint32_t o0 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0x00, 0xf, 0xf, false);
-  const uint32_t o1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0x55, 0xf, 0xf, false);
-  const uint32_t o2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xaa, 0xf, 0xf, false);
-  const uint32_t o3 = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0xff, 0xf, 0xf, false);
-  return ((o0 >> e) & 0x1111u) | (((o1 >> e) & 0x1111u) << 1) | (((o2 >> e) & 0x1111u) << 2) |
-         (((o3 >> e) & 0x1111u) << 3);
+  // rows v = q and q + 8 come from lane q of the group
+  return gather_keep_bits(own, e8, std::make_integer_sequence<int, 8>{});
 }
 // All ones when bit v of keep bits m is set, else 0 (one v_bfe_i32).
 __device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int)(m << (31 - v)) >> 31); }
@@ -718,17 +731,36 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
       u32x4_t zb[2];
       {
         float z[16];
-        if constexpr (DROP) {
+        if constexpr (DROP && ALIBI && MASK && D == 128) {
+          // every register in use: each lane makes the call of its own 8-key
+          // group and keeps its 4 fields (4g..4g+3), one group at a time
 #pragma unroll
           for (int vq = 0; vq < 4; ++vq) {
-            const int jq = n0 + nb * 32 + vq * 8 + g * 4;
-            const u32x4_t c = {(uint32_t)(jq >> 2), (uint32_t)i, (uint32_t)(b * p.Hq + hq), p.off_lo};
+            const u32x4_t c = {(uint32_t)((n0 + nb * 32 + vq * 8) >> 3), (uint32_t)i, (uint32_t)(b * p.Hq + hq),
+                               p.off_lo};
             const u32x4_t w = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+            const uint32_t w0 = g ? w[2] : w[0], w1 = g ? w[3] : w[1];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float dpk = w[e] < p.drop_thresh ? 0.f : dp[vq * 4 + e] * p.drop_scale;
+              const float dpk = keep_field(e < 2 ? w0 : w1, e & 1, p.drop_thresh) ? dp[vq * 4 + e] * p.drop_scale : 0.f;
               z[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - lse2) * (dpk - dlt);
             }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else if constexpr (DROP) {
+#pragma unroll
+          for (int vp = 0; vp < 2; ++vp) {  // 8-key groups vq = 2vp, 2vp + 1: one call per lane pair
+            uint32_t wq[2][2];
+            philox_pair_words((uint32_t)((n0 + nb * 32 + vp * 16) >> 3), (uint32_t)i, (uint32_t)(b * p.Hq + hq),
+                              p.off_lo, p.seed_lo ^ p.off_hi, p.seed_hi, g, wq[0], wq[1]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                const int v = (vp * 2 + h) * 4 + e;
+                const float dpk = keep_field(wq[h][e >> 1], e & 1, p.drop_thresh) ? dp[v] * p.drop_scale : 0.f;
+                z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dpk - dlt);
+              }
           }
         } else {
 #pragma unroll

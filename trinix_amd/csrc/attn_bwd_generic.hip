@@ -9,7 +9,7 @@
 //   dV = Pd^T dO,  dZ = P * (keep * (dO V^T) / (1 - p) - delta),
 //   dK = scale * dZ^T Q,  dQ = scale * dZ K,  delta = rowsum(dO * O),
 // keep being the forward's dropout mask, regenerated from the same Philox
-// counters (attn_params.h dropout_group).
+// counters (common.h keep_field).
 //
 // All products run on v_mfma_f32_32x32x2f32 (exact fp32 products, fp32
 // sums), so fp32 gradients keep fp32 accuracy.  The kernels work on 32x32
@@ -70,9 +70,10 @@ constexpr int kSP = 33;  // pitch of the 32x32 score tiles in LDS
 // -inf (no allowed key: the forward wrote NaN) gets zero gradients.
 __device__ inline void grad_group(const BwdParams& p, const Band& band, int bh, int i, int j, float lse2,
                                   float delta, float slope_l2, const char* mrow, float (&s)[4], float (&dp)[4]) {
+  // keys j..j+3 are fields (j % 8) + e of the call of their 8-key group
   u32x4_t rr = {0u, 0u, 0u, 0u};
   if (p.use_dropout)
-    rr = Philox::run((u32x4_t){(uint32_t)(j >> 2), (uint32_t)i, (uint32_t)bh, p.off_lo}, p.seed_lo ^ p.off_hi,
+    rr = Philox::run((u32x4_t){(uint32_t)(j >> 3), (uint32_t)i, (uint32_t)bh, p.off_lo}, p.seed_lo ^ p.off_hi,
                      p.seed_hi);
   const bool row_ok = i < p.Sq && lse2 != -INFINITY;
 #pragma unroll
@@ -83,7 +84,8 @@ __device__ inline void grad_group(const BwdParams& p, const Band& band, int bh, 
     if (p.alibi) z += slope_l2 * fabsf((float)(i - jj));
     if (p.mask && ok) z += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
     const float pr = ok ? exp2f(z) : 0.f;
-    const float keep = p.use_dropout ? (rr[e] < p.drop_thresh ? 0.f : p.drop_scale) : 1.f;
+    const int kf = (j & 7) + e;
+    const float keep = p.use_dropout ? (keep_field(rr[kf >> 1], kf & 1, p.drop_thresh) ? p.drop_scale : 0.f) : 1.f;
     s[e] = pr * keep;
     dp[e] = pr * (dp[e] * keep - delta);
   }

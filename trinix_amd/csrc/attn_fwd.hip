@@ -216,11 +216,19 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
     m_run = m_new;
     if (p.use_dropout) {
 #pragma unroll
-      for (int vq = 0; vq < 4; ++vq) {
-        float x[4] = {s[vq * 4 + 0], s[vq * 4 + 1], s[vq * 4 + 2], s[vq * 4 + 3]};
-        dropout_group(x, p, b * p.Hq + hq, i, n0 + vq * 8 + g * 4);
+      for (int vp = 0; vp < 2; ++vp) {  // 8-key groups vq = 2vp, 2vp + 1
+        float xa[4], xb[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s[vq * 4 + e] = x[e];
+        for (int e = 0; e < 4; ++e) {
+          xa[e] = s[vp * 8 + e];
+          xb[e] = s[vp * 8 + 4 + e];
+        }
+        dropout_pair(xa, xb, p, b * p.Hq + hq, i, n0 + vp * 16, g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          s[vp * 8 + e] = xa[e];
+          s[vp * 8 + 4 + e] = xb[e];
+        }
       }
     }
 #pragma unroll
@@ -375,8 +383,9 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.bm_cols = (int)((a->seqlen_k + 63) / 64);
   p.use_dropout = a->dropout_p > 0.f ? 1 : 0;
   {
-    const double th = (double)a->dropout_p * 4294967296.0;
-    p.drop_thresh = th >= 4294967295.0 ? 0xffffffffu : (uint32_t)th;
+    // dropped when the key's 16-bit Philox field < floor(p * 2^16)
+    const double th = (double)a->dropout_p * 65536.0;
+    p.drop_thresh = th >= 65535.0 ? 65535u : (uint32_t)th;
     p.drop_scale = a->dropout_p > 0.f ? 1.f / (1.f - a->dropout_p) : 1.f;
   }
   p.seed_lo = (uint32_t)a->dropout_seed;

@@ -557,12 +557,21 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-          float x[4] = {s[nb][vq * 4 + 0], s[nb][vq * 4 + 1], s[nb][vq * 4 + 2], s[nb][vq * 4 + 3]};
-          dropout_group(x, p, b * p.Hq + hq, i, n0 + nb * 32 + vq * 8 + g * 4);
+        for (int vp = 0; vp < 2; ++vp) {
+          // 8-key groups vq = 2vp, 2vp + 1: one Philox call per lane pair
+          float xa[4], xb[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) s[nb][vq * 4 + e] = x[e];
-          // with a mask too, one Philox group at a time (interleaved groups
+          for (int e = 0; e < 4; ++e) {
+            xa[e] = s[nb][vp * 8 + e];
+            xb[e] = s[nb][vp * 8 + 4 + e];
+          }
+          dropout_pair(xa, xb, p, b * p.Hq + hq, i, n0 + nb * 32 + vp * 16, g);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            s[nb][vp * 8 + e] = xa[e];
+            s[nb][vp * 8 + 4 + e] = xb[e];
+          }
+          // with a mask too, one Philox call at a time (interleaved calls
           // need more registers than the kernel has)
           if constexpr (MASK) __builtin_amdgcn_sched_barrier(0);
         }

@@ -31,7 +31,7 @@ struct FwdParams {
   int64_t bm_sb, bm_sh;
   int bm_cols;
   int use_dropout;
-  uint32_t drop_thresh;  // drop when the Philox word < drop_thresh
+  uint32_t drop_thresh;  // drop when the 16-bit Philox field < drop_thresh
   float drop_scale;      // 1 / (1 - p)
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
   const uint16_t* rope_cos;
@@ -83,14 +83,18 @@ __device__ inline void load_mask4(const void* base, int dtype, int j0, int64_t s
   }
 }
 
-// Dropout on keys j0..j0+3 of row i: p <- keep ? p/(1-p) : 0.  Counter
-// (j0/4, i, b*H+h, offset_lo), key (seed_lo ^ offset_hi, seed_hi); word e
-// decides key j0+e.
-__device__ inline void dropout_group(float* x, const FwdParams& p, int bh, int i, int j0) {
-  const u32x4_t c = {(uint32_t)(j0 >> 2), (uint32_t)i, (uint32_t)bh, p.off_lo};
-  const u32x4_t rr = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+// Dropout (common.h keep_field) on keys ga + 4g + e (xa) and ga + 8 + 4g + e
+// (xb), e = 0..3, of row i, ga % 8 == 0, g the lane half (the lane pair
+// l, l + 32 holds row i): p <- keep ? p / (1 - p) : 0.
+__device__ inline void dropout_pair(float (&xa)[4], float (&xb)[4], const FwdParams& p, int bh, int i, int ga, int g) {
+  uint32_t wa[2], wb[2];
+  philox_pair_words((uint32_t)(ga >> 3), (uint32_t)i, (uint32_t)bh, p.off_lo, p.seed_lo ^ p.off_hi, p.seed_hi, g, wa,
+                    wb);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) x[e] = (rr[e] < p.drop_thresh) ? 0.f : x[e] * p.drop_scale;
+  for (int e = 0; e < 4; ++e) {
+    xa[e] = keep_field(wa[e >> 1], e & 1, p.drop_thresh) ? xa[e] * p.drop_scale : 0.f;
+    xb[e] = keep_field(wb[e >> 1], e & 1, p.drop_thresh) ? xb[e] * p.drop_scale : 0.f;
+  }
 }
 
 // Combine a value with the one held by lane l ^ 32 (v_permlane32_swap).

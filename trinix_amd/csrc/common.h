@@ -130,4 +130,30 @@ struct Philox {
   }
 };
 
+// Dropout keep decisions.  One Philox call, counter (j/8, i, b*H+h,
+// offset_lo) and key (seed_lo ^ offset_hi, seed_hi), decides keys
+// 8*(j/8) .. +7 of row i: key 8m + k takes 16-bit field k of the four words
+// (word k/2, the low half for even k) and is kept when that field is at
+// least drop_thresh = floor(p * 2^16).
+__device__ inline bool keep_field(uint32_t w, int half, uint32_t th) { return (half ? (w >> 16) : (w & 0xffffu)) >= th; }
+
+// Keep words of two consecutive 8-key groups (c8, c8 + 1 in units of 8 keys)
+// of one row, for a lane pair (l, l + 32) that holds keys 4g .. 4g+3 of each
+// group (g = l / 32): lane half g makes the call of group c8 + g, and two
+// v_permlane32_swap hand each lane the two words of its own keys of both
+// groups (wa: group c8, wb: group c8 + 1; key 4g + e of a group is field e,
+// word e / 2).  One call per 8 elements; both lanes of every pair execute it.
+__device__ inline void philox_pair_words(uint32_t c8, uint32_t i, uint32_t bh, uint32_t off_lo, uint32_t k0,
+                                         uint32_t k1, int g, uint32_t (&wa)[2], uint32_t (&wb)[2]) {
+  const u32x4_t w = Philox::run((u32x4_t){c8 + (uint32_t)g, i, bh, off_lo}, k0, k1);
+  // swap(x, y): lanes 32..63 of x trade with lanes 0..31 of y, so the first
+  // result holds group c8's words in both halves and the second group c8+1's
+  const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+  wa[0] = s0[0];
+  wa[1] = s1[0];
+  wb[0] = s0[1];
+  wb[1] = s1[1];
+}
+
 }  // namespace trinix
