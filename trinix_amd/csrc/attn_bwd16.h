@@ -570,8 +570,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 // the MFMA rows, A operands from the K / V tiles in LDS; B operands the
 // lane's Q / dO rows in registers), dZ^T = P^T (dP^T - delta) in registers,
 // dQ^T += K^T dZ^T with K^T from LDS transpose reads.  With dropout (DROP)
-// dZ = P (keep dP/(1-p) - delta); a lane's 4 consecutive keys vq*8 + 4g +
-// 0..3 of a 32-key half are one Philox call of the forward's stream.
+// dZ = P (keep dP/(1-p) - delta), the keep bits drawn as the forward draws
+// them: the two lanes of a row share the calls of 8-key group pairs
+// (philox_pair_words).
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, bool DROP, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {

@@ -21,7 +21,7 @@
 //                     wavefront forms its partial S and dP over its columns,
 //                     the partials are summed through LDS, each thread turns
 //                     4 consecutive keys of one row into Pd and dZ (one
-//                     Philox call), and each wavefront accumulates its
+//                     Philox call, the 8-key group's), and each wavefront accumulates its
 //                     columns of dV += Pd^T dO and dK += dZ^T Q;
 //   bwd_dq_generic    one workgroup per (batch, q-head, 32 query rows), the
 //                     same with the Q/dO rows in registers and K/V tiles in
