@@ -503,3 +503,59 @@ def test_backward_long_context_one_row_band(case):
     for t in (hip[0][:, :r0], hip[0][:, r0 + 64:], hip[1][:, r0 + 64:], hip[2][:, r0 + 64:], hip[2][:, :lo]):
         assert int(torch.count_nonzero(t)) == 0  # outside the band's rows / keys: exactly zero
     _check(hip, eager, truth)
+
+
+DEAD_ROW_CASES = [
+    # (B, Sq, Sk, H, Hkv, D, dtype, kwargs): some query rows see no key
+    (1, 60, 40, 2, 1, 64, torch.bfloat16, dict(window_size=(5, 0))),          # rows >= 45: window past the keys
+    (2, 96, 96, 4, 2, 128, torch.float16, dict(alibi_slopes=orc.alibi_slopes(4), dead_mask=(7, 50, 51))),
+    (1, 80, 80, 2, 2, 64, torch.float32, dict(dead_mask=(0, 79), causal=True)),  # generic kernels (fp32)
+    (1, 70, 70, 2, 1, 256, torch.bfloat16, dict(window_size=(3, 3), dead_mask=(33,))),  # generic (D=256)
+]
+
+
+def _dead_row_inputs(case):
+    B, Sq, Sk, H, Hkv, D, dtype, kw = case
+    kw = dict(kw)
+    dead_rows = kw.pop("dead_mask", None)
+    if dead_rows is not None:
+        g = torch.Generator().manual_seed(151)
+        m = torch.randn(Sq, Sk, generator=g) * 0.5
+        m[list(dead_rows), :] = float("-inf")
+        kw["attn_mask"] = m
+    return B, Sq, Sk, H, Hkv, D, dtype, kw
+
+
+@pytest.mark.parametrize("case", range(len(DEAD_ROW_CASES)))
+def test_backward_rows_without_allowed_keys(case):
+    """Rows with no allowed key (a window past the keys, a mask row of -inf)
+    give NaN outputs, as eager does; eager autograd then makes the whole
+    (batch, head)'s gradients NaN, the HIP backward gives those rows zero
+    gradient.  Checked: every gradient finite, dq of those rows exactly 0,
+    and all gradients equal (backward bar) to autograd of the same scores
+    with those rows made visible and their dO set to 0, in fp64 and in the
+    input dtype."""
+    B, Sq, Sk, H, Hkv, D, dtype, kw = _dead_row_inputs(DEAD_ROW_CASES[case])
+    q, k, v, do = _inputs(B, Sq, Sk, H, Hkv, D, seed=150 + case)
+    out, hip = _hip_grads(q, k, v, do, dtype, **kw)
+    bias = torch.from_numpy(orc._bias64(Sq, Sk, H, B, kw.get("attn_mask"), kw.get("causal", False),
+                                        kw.get("window_size"), kw.get("alibi_slopes")))
+    dead = torch.isinf(bias).all(-1)  # (B, H, Sq)
+    assert dead.any()
+    assert torch.isnan(out.permute(0, 2, 1, 3)[dead]).all()
+    assert all(torch.isfinite(h).all() for h in hip)
+    assert int(torch.count_nonzero(hip[0].permute(0, 2, 1, 3)[dead])) == 0
+    live_bias = bias.masked_fill(dead[..., None], 0.0)  # dead rows made visible ...
+    do_live = do.permute(0, 2, 1, 3).masked_fill(dead[..., None], 0.0).permute(0, 2, 1, 3)  # ... with dO = 0
+
+    def grads(dt):
+        xs = [t.detach().to(dt).clone().requires_grad_(True) for t in (q, k, v)]
+        G = H // Hkv
+        kk = xs[1].repeat_interleave(G, dim=2).transpose(1, 2)
+        vv = xs[2].repeat_interleave(G, dim=2).transpose(1, 2)
+        s = torch.matmul(xs[0].transpose(1, 2), kk.transpose(-1, -2)) * D ** -0.5 + live_bias.to(dt)
+        o = torch.matmul(torch.softmax(s.double(), dim=-1).to(dt), vv).transpose(1, 2)
+        o.backward(do_live.to(dt))
+        return [x.grad.double() for x in xs]
+
+    _check(hip, grads(dtype), grads(torch.float64))

@@ -23,6 +23,7 @@
 // the input dtype for their products, as in the forward.  bwd_dkdv also takes
 // dZ = P (dP - delta) from the rounded P (bwd_dq from the fp32 one).
 #pragma once
+#include <cfloat>
 #include <climits>
 #include <utility>
 
@@ -441,8 +442,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
           const f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
+          // rows with no allowed key: lse -inf and every score -inf; the
+          // floor (finite after the scaling) keeps P at 0 instead of NaN
 #pragma unroll
-          for (int e = 0; e < 4; ++e) x[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - l4[e] * kLog2e);
+          for (int e = 0; e < 4; ++e)
+            x[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - fmaxf(l4[e], -0.5f * FLT_MAX) * kLog2e);
         }
         u32x4_t pb[2];
 #pragma unroll
@@ -619,7 +623,9 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
     }
   }
   const int64_t vo = ((int64_t)b * p.Hq + hq) * p.Sq + ic;
-  const float lse2 = p.lse[vo] * kLog2e;
+  // a row with no allowed key has lse -inf and every score -inf: a finite
+  // floor keeps exp2(score - lse2) at 0 instead of exp2(-inf + inf) = NaN
+  const float lse2 = fmaxf(p.lse[vo] * kLog2e, -FLT_MAX);
   const float dlt = p.delta[vo];
   float slope_l2 = 0.f;
   if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;

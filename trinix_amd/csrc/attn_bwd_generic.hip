@@ -114,7 +114,9 @@ __global__ __launch_bounds__(256) void bwd_delta_generic(const BwdParams p, int6
   for (int d = lane; d < D; d += 64) acc += Elem<T>::ld(p.o, oo + d) * Elem<T>::ld(p.dout, od + d);
 #pragma unroll
   for (int m = 32; m >= 1; m /= 2) acc += __shfl_xor(acc, m);
-  if (lane == 0) p.delta[row] = acc;
+  // a row with no allowed key (lse -inf, NaN output): delta 0, so that its
+  // gradients are 0 rather than 0 * NaN
+  if (lane == 0) p.delta[row] = p.lse[row] == -INFINITY ? 0.f : acc;
 }
 
 template <class T, int D>
