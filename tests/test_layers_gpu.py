@@ -93,3 +93,72 @@ def test_functional_forward_attention_gqa_unrepeated():
     assert torch.equal(a, b)
     ref = orc.functional_attention(q.cpu(), k.cpu(), v.cpu(), causal=True)
     assert ((a.cpu() - ref).abs().max() / ref.abs().max()).item() <= 1e-5
+
+
+def _layer_case(seed):
+    import random
+
+    r = random.Random(70_000 + seed)
+    kind = r.choice(["mha", "gqa", "mqa", "mhsa"])
+    D, H = r.choice([64, 128]), r.choice([2, 4])
+    dtype = r.choice([torch.float32, torch.bfloat16])
+    kw = dict(causal=r.random() < 0.6)
+    pm = r.choice(["none", "rope", "alibi"])
+    kw["position_method"] = pm
+    if pm == "rope":
+        kw["rope_base"] = r.choice([10000.0, 500000.0])
+    if r.random() < 0.3 and kw["causal"]:
+        kw.update(use_sliding_window=True, sliding_window_size=r.randint(4, 60))
+    if r.random() < 0.4 and kind != "mhsa":
+        kw.update(qk_norm=True, qk_norm_type=r.choice(["rmsnorm", "layernorm"]))
+    return kind, D * H, H, dtype, kw, r.choice([1, 2]), r.randint(2, 200), r.random() < 0.5, r.random() < 0.5
+
+
+@pytest.mark.parametrize("seed", list(range(30)))
+def test_random_layer_flash_matches_pytorch_backend(seed):
+    """Seeded random layer configurations (class, head_dim, heads, dtype,
+    causal, RoPE / ALiBi, sliding window, qk-norm type): the HIP path
+    (kernel_type='flash') against the layer's own eager backend
+    (kernel_type='pytorch', the restated reference path) with the same
+    weights.  Forward output, and either the gradients of the input and of
+    every parameter (training) or three cached decode steps after a prefill
+    (inference).  Bars: 1e-4 (fp32) / 3e-2 (bf16) of max(1, |out|) for
+    outputs; 2e-4 / 5e-2 of the largest gradient for gradients (the key
+    bias's own gradient is 0 up to rounding)."""
+    kind, E, H, dtype, kw, B, S, train, decode = _layer_case(seed)
+    print(f"seed {seed}: {kind} E{E} H{H} {dtype} B{B} S{S} train={train} {kw}", flush=True)
+    torch.manual_seed(seed)
+    hip = _make(kind, E, H, kernel_type="flash", **kw)[0].cuda().to(dtype)
+    ref = _make(kind, E, H, kernel_type="pytorch", **kw)[0].cuda().to(dtype)
+    ref.load_state_dict(hip.state_dict())
+    x = torch.randn(B, S, E, device="cuda", dtype=dtype)
+    tol, gtol = (1e-4, 2e-4) if dtype == torch.float32 else (3e-2, 5e-2)
+    res = []
+    for m in (hip, ref):
+        xx = x.detach().clone().requires_grad_(train)
+        o = m(xx)
+        o = o[0] if isinstance(o, tuple) else o
+        grads = None
+        if train:
+            o.float().square().mean().backward()
+            grads = [xx.grad.float()] + [p.grad.float() for p in m.parameters() if p.grad is not None]
+        res.append((o.detach().float(), grads))
+    (oh, gh), (orf, gr) = res
+    assert (oh - orf).abs().max().item() <= tol * max(1.0, orf.abs().max().item())
+    if train:
+        assert len(gh) == len(gr)
+        assert (gh[0] - gr[0]).abs().max().item() <= gtol * gr[0].abs().max().item()
+        pscale = max(t.abs().max().item() for t in gr[1:])
+        for a, b in zip(gh[1:], gr[1:]):
+            assert (a - b).abs().max().item() <= gtol * pscale
+    elif decode and kind != "mhsa" and S > 4:
+        steps = []
+        with torch.no_grad():
+            for m in (hip, ref):
+                _, cache = m(x[:, :-3], use_cache=True)[:2]
+                outs = []
+                for t in range(3):
+                    o1, cache = m(x[:, S - 3 + t:S - 2 + t], past_key_value=cache, use_cache=True)[:2]
+                    outs.append(o1.float())
+                steps.append(torch.cat(outs, 1))
+        assert (steps[0] - steps[1]).abs().max().item() <= tol * max(1.0, steps[1].abs().max().item())
