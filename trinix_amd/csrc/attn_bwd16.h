@@ -439,14 +439,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
             x[v] = qspan.ok(i) ? x[v] : -INFINITY;
           }
         }
+        // Rows with no allowed key have lse -inf and every score -inf; a
+        // finite floor on lse (finite after the scaling) keeps their P at 0
+        // instead of exp2(-inf + inf) = NaN.  Such a row can only sit in a
+        // sub-tile the band cuts or whose mask is read.
+        const bool may_dead = !full || (MASK && mcode > 0);
 #pragma unroll
         for (int vq = 0; vq < 4; ++vq) {
-          const f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
-          // rows with no allowed key: lse -inf and every score -inf; the
-          // floor (finite after the scaling) keeps P at 0 instead of NaN
+          f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
+          if (may_dead)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            x[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - fmaxf(l4[e], -0.5f * FLT_MAX) * kLog2e);
+            for (int e = 0; e < 4; ++e) l4[e] = fmaxf(l4[e], -0.5f * FLT_MAX);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - l4[e] * kLog2e);
         }
         u32x4_t pb[2];
 #pragma unroll
