@@ -19,7 +19,8 @@ template <class E, int D>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(const uint16_t* __restrict__ o, int64_t o_sb, int64_t o_ss,
                                                         int64_t o_sh, const uint16_t* __restrict__ dout, int64_t do_sb,
                                                         int64_t do_ss, int64_t do_sh, const float* __restrict__ lse,
-                                                        float* __restrict__ delta, int Hq, int Sq, int64_t rows) {
+                                                        float* __restrict__ delta, float dmul, int Hq, int Sq,
+                                                        int64_t rows) {
   constexpr int LPR = D / 8, RPB = 256 / LPR;
   const int64_t row = (int64_t)blockIdx.x * RPB + threadIdx.x / LPR;
   const int t = threadIdx.x % LPR;
@@ -38,7 +39,9 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const uint16_t* __restri
   for (int m = LPR / 2; m >= 1; m /= 2) acc += __shfl_xor(acc, m);
   // a row with no allowed key (lse -inf) has a NaN output and P = 0: its
   // delta is 0, so that its dZ = P (dP - delta) is 0 rather than 0 * NaN
-  if (t == 0 && row < rows) delta[row] = lse[row] == -INFINITY ? 0.f : acc;
+  // dmul = 1 - p with dropout: the kernels then use keep*dP - delta*(1-p)
+  // and apply 1/(1-p) to dq and dk in their epilogues
+  if (t == 0 && row < rows) delta[row] = lse[row] == -INFINITY ? 0.f : acc * dmul;
 }
 
 template <class E, int D>
@@ -46,7 +49,8 @@ hipError_t launch_delta(const BwdParams& p, hipStream_t st) {
   constexpr int RPB = 256 / (D / 8);
   const int64_t rows = (int64_t)p.B * p.Hq * p.Sq;
   return launch_kernel(&bwd_delta_kernel<E, D>, dim3((unsigned)((rows + RPB - 1) / RPB)), dim3(256), 0, st, p.o,
-                       p.o_sb, p.o_ss, p.o_sh, p.dout, p.do_sb, p.do_ss, p.do_sh, p.lse, p.delta, p.Hq, p.Sq, rows);
+                       p.o_sb, p.o_ss, p.o_sh, p.dout, p.do_sb, p.do_ss, p.do_sh, p.lse, p.delta,
+                       p.use_dropout ? 1.f / p.drop_scale : 1.f, p.Hq, p.Sq, rows);
 }
 
 }  // namespace

@@ -206,9 +206,11 @@ __device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int
 // item orders all of it.  The loop runs six steps per trip so that every slot
 // index is a compile-time constant (LDS addresses as immediate offsets).
 // With dropout (DROP), stage A regenerates the keep bits of its sub-tile,
-// takes dV^T += dO^T Pd with Pd = keep ? P/(1-p) : 0, and hands the bits to
-// stage B through LDS next to P; stage B takes dZ = P (keep dP/(1-p) - delta)
-// (delta = rowsum(dO*O) is unchanged by dropout).
+// takes dV^T += dO^T (keep ? P : 0), and hands the bits to stage B through
+// LDS next to P; stage B takes dZ' = P (keep dP - delta (1-p)), the delta
+// kernel having scaled delta = rowsum(dO*O) by 1-p.  The 1/(1-p) of
+// Pd = keep P/(1-p) and of dZ = P (keep dP/(1-p) - delta) = dZ'/(1-p) is
+// applied once per output element in the epilogue.
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
@@ -465,7 +467,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
           const uint32_t km = keep_bits_of_key(p, b * p.Hq + hq, j, i0 + st * 32 + g * 4);
           *m_slot(PS, st) = km;
 #pragma unroll
-          for (int v = 0; v < 16; ++v) x[v] = __uint_as_float(__float_as_uint(x[v] * p.drop_scale) & keep_word(km, v));
+          for (int v = 0; v < 16; ++v) x[v] = __uint_as_float(__float_as_uint(x[v]) & keep_word(km, v));
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk)
             pb[kk] = (u32x4_t){E::pack(x[kk * 8 + 0], x[kk * 8 + 1]), E::pack(x[kk * 8 + 2], x[kk * 8 + 3]),
@@ -495,9 +497,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         u32x4_t zb[2];
         uint32_t km = 0;
         if constexpr (DROP) km = *m_slot(PS, st);
-        // dP of the dropped P: keep ? dP/(1-p) : 0 (DROP)
+        // dP of the dropped P, without its 1/(1-p) (epilogue): keep ? dP : 0
         auto dpk = [&](int v) __attribute__((always_inline)) {
-          if constexpr (DROP) return __uint_as_float(__float_as_uint(dp[v] * p.drop_scale) & keep_word(km, v));
+          if constexpr (DROP) return __uint_as_float(__float_as_uint(dp[v]) & keep_word(km, v));
           else return dp[v];
         };
 #pragma unroll
@@ -557,7 +559,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
     if (j < p.Sk) {
       uint16_t* row = SB ? p.dk + b * p.dk_sb + hkv * p.dk_sh + (int64_t)j * p.dk_ss
                          : p.dv + b * p.dv_sb + hkv * p.dv_sh + (int64_t)j * p.dv_ss;
-      const float f = SB ? p.scale : 1.f;
+      // with dropout the 1/(1-p) of Pd (dV) and of keep*dP (dK; delta comes
+      // scaled by 1-p) is applied here, once per output element
+      const float f = (SB ? p.scale : 1.f) * (DROP ? p.drop_scale : 1.f);
 #pragma unroll
       for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -579,9 +583,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 // the MFMA rows, A operands from the K / V tiles in LDS; B operands the
 // lane's Q / dO rows in registers), dZ^T = P^T (dP^T - delta) in registers,
 // dQ^T += K^T dZ^T with K^T from LDS transpose reads.  With dropout (DROP)
-// dZ = P (keep dP/(1-p) - delta), the keep bits drawn as the forward draws
-// them: the two lanes of a row share the calls of 8-key group pairs
-// (philox_pair_words).
+// dZ' = P (keep dP - delta (1-p)) (delta scaled by the delta kernel) and
+// the 1/(1-p) of dZ = dZ'/(1-p) applied in the epilogue; the keep bits are
+// drawn as the forward draws them: the two lanes of a row share the calls
+// of 8-key group pairs (philox_pair_words).
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, bool DROP, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
@@ -754,7 +759,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
             const uint32_t w0 = g ? w[2] : w[0], w1 = g ? w[3] : w[1];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float dpk = keep_field(e < 2 ? w0 : w1, e & 1, p.drop_thresh) ? dp[vq * 4 + e] * p.drop_scale : 0.f;
+              const float dpk = keep_field(e < 2 ? w0 : w1, e & 1, p.drop_thresh) ? dp[vq * 4 + e] : 0.f;
               z[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - lse2) * (dpk - dlt);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -770,7 +775,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int v = (vp * 2 + h) * 4 + e;
-                const float dpk = keep_field(wq[h][e >> 1], e & 1, p.drop_thresh) ? dp[v] * p.drop_scale : 0.f;
+                const float dpk = keep_field(wq[h][e >> 1], e & 1, p.drop_thresh) ? dp[v] : 0.f;
                 z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dpk - dlt);
               }
           }
@@ -834,13 +839,16 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 
   if (i < p.Sq) {
     uint16_t* qrow = p.dq + b * p.dq_sb + hq * p.dq_sh + (int64_t)i * p.dq_ss;
+    // with dropout the 1/(1-p) of keep*dP (delta comes scaled by 1-p) is
+    // applied here, once per output element
+    const float f = DROP ? p.scale * p.drop_scale : p.scale;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int vq = 0; vq < 4; ++vq) {
         const int d0 = db * 32 + vq * 8 + g * 4;
-        *(u32x2_t*)(qrow + d0) = (u32x2_t){E::pack(acc[db][vq * 4 + 0] * p.scale, acc[db][vq * 4 + 1] * p.scale),
-                                           E::pack(acc[db][vq * 4 + 2] * p.scale, acc[db][vq * 4 + 3] * p.scale)};
+        *(u32x2_t*)(qrow + d0) = (u32x2_t){E::pack(acc[db][vq * 4 + 0] * f, acc[db][vq * 4 + 1] * f),
+                                           E::pack(acc[db][vq * 4 + 2] * f, acc[db][vq * 4 + 3] * f)};
       }
   }
 }
