@@ -244,12 +244,14 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
   const float l = l_run + __shfl_xor(l_run, 32);
   if (i < p.Sq) {
     float* orow = o + b * p.o_sb + hq * p.o_sh + (int64_t)i * p.o_ss;
+    // with dropout, the 1/(1-p) of the kept weights (dropout_pair)
+    const float os = p.use_dropout ? p.drop_scale : 1.f;
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int d = db * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
-        orow[d] = acc[db][v] / l;
+        orow[d] = acc[db][v] * os / l;
       }
     if (p.lse && g == 0) p.lse[((int64_t)b * p.Hq + hq) * p.Sq + i] = (m_run + log2f(l)) * kLn2;
   }

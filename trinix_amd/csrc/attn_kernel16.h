@@ -717,7 +717,8 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
   asm volatile("" : "+v"(ie), "+v"(ge));
   const float l = xlane_sum(l_run);
   if (ie < p.Sq && kp == 0) {
-    const float inv = 1.f / l;
+    // with dropout, the 1/(1-p) of the kept weights (dropout_pair)
+    const float inv = (DROP ? p.drop_scale : 1.f) / l;
     uint16_t* orow = p.o + b * p.o_sb + hq * p.o_sh + (int64_t)ie * p.o_ss;
 #pragma unroll
     for (int db = 0; db < DB; ++db)

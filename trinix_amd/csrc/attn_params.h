@@ -85,15 +85,16 @@ __device__ inline void load_mask4(const void* base, int dtype, int j0, int64_t s
 
 // Dropout (common.h keep_field) on keys ga + 4g + e (xa) and ga + 8 + 4g + e
 // (xb), e = 0..3, of row i, ga % 8 == 0, g the lane half (the lane pair
-// l, l + 32 holds row i): p <- keep ? p / (1 - p) : 0.
+// l, l + 32 holds row i): p <- keep ? p : 0.  The 1/(1-p) of the kept
+// weights is applied to the output once, in the kernels' epilogues.
 __device__ inline void dropout_pair(float (&xa)[4], float (&xb)[4], const FwdParams& p, int bh, int i, int ga, int g) {
   uint32_t wa[2], wb[2];
   philox_pair_words((uint32_t)(ga >> 3), (uint32_t)i, (uint32_t)bh, p.off_lo, p.seed_lo ^ p.off_hi, p.seed_hi, g, wa,
                     wb);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    xa[e] = keep_field(wa[e >> 1], e & 1, p.drop_thresh) ? xa[e] * p.drop_scale : 0.f;
-    xb[e] = keep_field(wb[e >> 1], e & 1, p.drop_thresh) ? xb[e] * p.drop_scale : 0.f;
+    xa[e] = keep_field(wa[e >> 1], e & 1, p.drop_thresh) ? xa[e] : 0.f;
+    xb[e] = keep_field(wb[e >> 1], e & 1, p.drop_thresh) ? xb[e] : 0.f;
   }
 }
 
