@@ -115,7 +115,8 @@ typedef struct trinix_attn_fwd_args {
   int64_t alibi_stride[2];
   const void* mask;             /* additive mask, NULL = none */
   int32_t mask_dtype;           /* trinix_dtype */
-  int64_t mask_stride[4];       /* b, h, i, j (0 = broadcast); 0 <= (seqlen_k-1)*j < 2^31 */
+  int64_t mask_stride[4];       /* b, h, i, j: each >= 0 (0 = broadcast), */
+                                /* (seqlen_k-1)*j < 2^31, min(seqlen_q-1, 31)*i < 2^31 */
   const uint8_t* mask_blockmap; /* from trinix_attn_mask_blockmap, or NULL */
   int64_t blockmap_stride[2];   /* b, h strides of the block map (0 = broadcast) */
   /* Dropout on the attention weights: key j of row i of (b, h) is dropped
@@ -175,7 +176,8 @@ int trinix_attn_fwd_splitkv(const trinix_attn_fwd_args* args, void* workspace,
  * static device array of TRINIX_SPLITKV_SCRATCH_BYTES that the library holds
  * on every GPU it runs on until the process ends (its address is looked up
  * once per device).  Same arguments, semantics and output as
- * trinix_attn_fwd_splitkv; `stream` must belong to the current device.
+ * trinix_attn_fwd_splitkv; `stream` must belong to the current device
+ * (TRINIX_ERR_BAD_ARGUMENT otherwise, before any launch).
  * Returns TRINIX_ERR_SCRATCH_TOO_SMALL when the plan's workspace exceeds the
  * array (the default plan needs at most about 17 MB), before any launch.
  * Every call on one GPU shares that GPU's array: calls that overlap on one

@@ -67,6 +67,16 @@ static trinix_attn_fwd_args valid_fwd() {
   return a;
 }
 
+template <class Args>
+static void set_mask(Args& x, int64_t sb, int64_t sh, int64_t si, int64_t sj) {
+  x.mask = (const void*)4096;
+  x.mask_dtype = TRINIX_F32;
+  x.mask_stride[0] = sb;
+  x.mask_stride[1] = sh;
+  x.mask_stride[2] = si;
+  x.mask_stride[3] = sj;
+}
+
 static trinix_attn_bwd_args valid_bwd() {
   trinix_attn_bwd_args a;
   std::memset(&a, 0, sizeof(a));
@@ -131,6 +141,13 @@ int main() {
         {[](trinix_attn_fwd_args& x) { x.rope_cos = (void*)4096; }, TRINIX_ERR_NULL_POINTER},
         {[](trinix_attn_fwd_args& x) { x.mask = (void*)4096; x.mask_dtype = 9; }, TRINIX_ERR_BAD_DTYPE},
         {[](trinix_attn_fwd_args& x) { x.q_norm_weight = (void*)4096; x.dropout_p = 0.1f; }, TRINIX_ERR_BAD_ARGUMENT},
+        // mask strides: non-negative; a 32-row sub-tile's rows at 32-bit offsets
+        {[](trinix_attn_fwd_args& x) { set_mask(x, 0, 0, -64, 1); }, TRINIX_ERR_BAD_STRIDE},
+        {[](trinix_attn_fwd_args& x) { set_mask(x, -4096, 0, 64, 1); }, TRINIX_ERR_BAD_STRIDE},
+        {[](trinix_attn_fwd_args& x) { set_mask(x, 0, 0, 1ll << 27, 1); }, TRINIX_ERR_BAD_STRIDE},
+        {[](trinix_attn_fwd_args& x) { set_mask(x, 0, 0, (1ll << 31) / 31, 1); }, TRINIX_OK},
+        {[](trinix_attn_fwd_args& x) { set_mask(x, 0, 0, 64, 1ll << 26); }, TRINIX_ERR_BAD_STRIDE},
+        {[](trinix_attn_fwd_args& x) { x.seqlen_q = 1; set_mask(x, 0, 0, 1ll << 40, 1); }, TRINIX_OK},
     };
     for (const Case& c : table) {
       trinix_attn_fwd_args x = valid_fwd();
@@ -156,7 +173,22 @@ int main() {
     a = valid_bwd();
     a.dk_stride[1] = std::numeric_limits<int64_t>::max();
     CHECK(validate_bwd_args(&a) == TRINIX_ERR_BAD_STRIDE, "bwd stride");
-    cases += 5;
+    // the dK/dV kernel reads a mask sub-tile's 32 rows at 32-bit offsets
+    // r * row_stride from its first row (64-bit): (Sq = 64) 31 * stride < 2^31
+    a = valid_bwd();
+    set_mask(a, 0, 0, (1ll << 31) / 31 + 1, 1);
+    CHECK(validate_bwd_args(&a) == TRINIX_ERR_BAD_STRIDE, "bwd mask row stride");
+    a = valid_bwd();
+    set_mask(a, 0, 0, (1ll << 31) / 31, 1);
+    CHECK(validate_bwd_args(&a) == TRINIX_OK, "bwd mask row stride at the limit");
+    a = valid_bwd();
+    set_mask(a, 0, 0, -1, 1);
+    CHECK(validate_bwd_args(&a) == TRINIX_ERR_BAD_STRIDE, "bwd negative mask row stride");
+    a = valid_bwd();
+    a.seqlen_q = a.seqlen_k = 70000;  // a contiguous mask beyond 2^32 elements
+    set_mask(a, 0, 0, 70000, 1);
+    CHECK(validate_bwd_args(&a) == TRINIX_OK, "bwd contiguous mask of 70000^2");
+    cases += 9;
   }
   // ---- the tuning override TRINIX_ATTN_CFG="nw,occ,bn[,ks]": ks 0 (the
   // per-item split), 1 and 2 are taken, anything else leaves the planner's
@@ -243,7 +275,15 @@ int main() {
     a.dtype = (int32_t)(next_u64() % 4);
     for (int i = 0; i < 4; ++i)
       if (next_u64() % 4 == 0) a.dk_stride[i] = rand_size();
+    if (next_u64() % 2 == 0) set_mask(a, rand_size(), rand_size(), rand_size(), rand_size());
     if (validate_bwd_args(&a) != TRINIX_OK) continue;
+    if (a.mask) {
+      // what the kernels' mask addressing relies on (see mask_strides_ok)
+      for (int i = 0; i < 4; ++i) CHECK(a.mask_stride[i] >= 0, "accepted mask stride >= 0");
+      const int64_t rows = a.seqlen_q - 1 < 31 ? a.seqlen_q - 1 : 31;
+      CHECK((__int128)rows * a.mask_stride[2] < ((__int128)1 << 31), "sub-tile row offsets fit 31 bits");
+      CHECK((__int128)(a.seqlen_k - 1) * a.mask_stride[3] < ((__int128)1 << 31), "key offsets fit 31 bits");
+    }
     const bool masked = next_u64() % 2 == 0;
     if (pick_dq_wide(a.head_dim, a.batch, a.nheads_q, a.seqlen_q, a.causal || a.has_window, masked))
       CHECK(a.head_dim == 128 && !masked, "wide dQ only at head_dim 128 without a mask");

@@ -92,6 +92,11 @@ def assert_parity_full(out, ref, dtype, what, q, k, v, row0=0, **kw):
     mean = d[ok].mean().item()
     assert mean <= 2e-3, f"{what}: mean abs {mean:.4g} (<=2e-3)"
     bad = (d > 2e-2).nonzero().tolist()
+    # the adjudication below is for isolated roundings, not a second bar: at
+    # most one element in 10^7 (C3 had 1 of 268M) may need it
+    limit = max(8, out.numel() // 10 ** 7)
+    print(f"{what}: {len(bad)} element(s) beyond 2e-2 of the oracle (limit {limit})", flush=True)
+    assert len(bad) <= limit, f"{what}: {len(bad)} elements beyond 2e-2 of the oracle (limit {limit})"
     rows = {}
     for b, i, h, _ in bad:
         rows.setdefault((b, h), set()).add(i)

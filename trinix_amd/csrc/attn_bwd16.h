@@ -410,7 +410,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         if constexpr (MASK) {
           if (mcode > 0) {
             const int esz = p.mask_dtype == TRINIX_F32 ? 4 : (p.mask_dtype == TRINIX_U8 ? 1 : 2);
-            mrow = (const char*)p.mask + (b * p.mk_sb + hq * p.mk_sh + (int64_t)jc * p.mk_sj) * esz;
+            // the sub-tile's first row in 64 bits; its 32 rows then sit at
+            // 32-bit offsets r * mk_si, r < 32 (the host bounds 31 * mk_si)
+            mrow = (const char*)p.mask +
+                   (b * p.mk_sb + hq * p.mk_sh + (int64_t)jc * p.mk_sj + (int64_t)(i0 + st * 32) * p.mk_si) * esz;
           }
         }
         float x[16];
@@ -423,12 +426,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         if constexpr (MASK) {
           // rows vq*8 + 4g + 0..3 of the sub-tile: 4 consecutive rows per
           // load group, one dtype switch per group (rows past Sq read row
-          // Sq-1; they are masked below)
+          // Sq-1; they are masked below).  A live sub-tile starts at a row
+          // < Sq, so the last row's offset within it is in [0, 31].
           if (mcode > 0) {
+            const int rlast = min(31, p.Sq - 1 - (i0 + st * 32));
 #pragma unroll
             for (int vq = 0; vq < 4; ++vq) {
               float mv[4];
-              load_mask4(mrow, p.mask_dtype, i0 + st * 32 + vq * 8 + g * 4, p.mk_si, p.Sq - 1, mv);
+              load_mask4(mrow, p.mask_dtype, vq * 8 + g * 4, p.mk_si, rlast, mv);
 #pragma unroll
               for (int e = 0; e < 4; ++e) x[vq * 4 + e] += mv[e] * kLog2e;
             }

@@ -458,9 +458,17 @@ static __device__ __align__(256) float scratch[TRINIX_SPLITKV_SCRATCH_BYTES / si
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_on_current_device(void** out) {
+// The scratch of the current device, which must be the device of `stream`
+// (the kernels run on the stream's device, and each device holds its own
+// copy of the array at its own address).  The null stream belongs to the
+// current device.
+int scratch_for_stream(hipStream_t stream, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return TRINIX_ERR_NO_DEVICE;
+  if (stream) {
+    int sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) return TRINIX_ERR_BAD_ARGUMENT;
+  }
   std::lock_guard<std::mutex> guard(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* ptr = nullptr;
@@ -493,7 +501,7 @@ extern "C" int trinix_attn_fwd_splitkv_noalloc(const trinix_attn_fwd_args* a, vo
   if (pl.ws_bytes > (int64_t)TRINIX_SPLITKV_SCRATCH_BYTES) return TRINIX_ERR_SCRATCH_TOO_SMALL;
   void* ws = nullptr;
   if (pl.ws_bytes > 0) {
-    const int src = scratch_on_current_device(&ws);
+    const int src = scratch_for_stream((hipStream_t)stream, &ws);
     if (src != TRINIX_OK) return src;
   }
   return launch_splitkv(a, pl, ws, (hipStream_t)stream);

@@ -57,8 +57,9 @@ __device__ inline float load_mask_elem(const void* base, int dtype, int64_t idx)
 // Mask values of keys j0..j0+3 (element stride sj) of one row: one
 // wave-uniform dtype switch for the four loads, keys past jmax read key jmax
 // (their scores are masked anyway), so the loads carry no branches.  The
-// element offsets within a row are 32-bit: the host requires
-// 0 <= (Sk - 1) * sj < 2^31 (check_mask_stride).
+// element offsets are 32-bit: the host requires 0 <= (Sk - 1) * sj < 2^31
+// for a key stride, and 0 <= min(Sq - 1, 31) * si < 2^31 for a row stride
+// read within a 32-row sub-tile (mask_strides_ok, host_plan.cpp).
 __device__ inline void load_mask4(const void* base, int dtype, int j0, int64_t sj, int jmax, float (&mv)[4]) {
   uint32_t idx[4];
 #pragma unroll

@@ -146,6 +146,17 @@ static bool mask_key_stride_ok(int64_t sj, int64_t sk) {
   return sj >= 0 && (sk <= 1 || sj <= ((1ll << 31) - 1) / (sk - 1));  // (sk - 1) * sj < 2^31, no overflow
 }
 
+// Every mask stride is a non-negative element count (0 = broadcast); the
+// batch, head and row parts of an address are formed in 64 bits.  The dK/dV
+// kernel reads the 32 rows of a query sub-tile at 32-bit offsets r * si from
+// the sub-tile's first row (r < 32, and r <= Sq - 1).
+static bool mask_strides_ok(const int64_t st[4], int64_t sq, int64_t sk) {
+  if (st[0] < 0 || st[1] < 0 || st[2] < 0) return false;
+  const int64_t rows = sq - 1 < 31 ? sq - 1 : 31;
+  if (rows > 0 && st[2] > ((1ll << 31) - 1) / rows) return false;
+  return mask_key_stride_ok(st[3], sk);
+}
+
 int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (!a) return TRINIX_ERR_NULL_POINTER;
   const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
@@ -170,7 +181,7 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
       a->mask_dtype != TRINIX_U8)
     return TRINIX_ERR_BAD_DTYPE;
   if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
-  if (a->mask && !mask_key_stride_ok(a->mask_stride[3], a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
+  if (a->mask && !mask_strides_ok(a->mask_stride, a->seqlen_q, a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
   if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
   if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
   if (a->rope_cos && esize == 2 &&
@@ -207,7 +218,7 @@ int validate_bwd_args(const trinix_attn_bwd_args* a) {
       a->mask_dtype != TRINIX_U8)
     return TRINIX_ERR_BAD_DTYPE;
   if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
-  if (a->mask && !mask_key_stride_ok(a->mask_stride[3], a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
+  if (a->mask && !mask_strides_ok(a->mask_stride, a->seqlen_q, a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
   return TRINIX_OK;
 }
 

@@ -93,6 +93,8 @@ def _prepare_operand(t: torch.Tensor, d_kernel: int) -> torch.Tensor:
         t = torch.nn.functional.pad(t, (0, d_kernel - d))
     if not _kernel_ready(t):
         t = t.contiguous()
+        if not _kernel_ready(t):  # contiguous already, but its start is not 16-byte aligned
+            t = t.clone()
     return t
 
 
@@ -107,15 +109,21 @@ class TritonAttentionKernel:
             attention forward; see the module docstring.
     """
 
+    _available = False  # set once a check has passed; every call re-checks until then
+
     @staticmethod
     def is_available() -> bool:
+        if TritonAttentionKernel._available:
+            return True
         try:
             lib = nat.load_library()
         except (RuntimeError, OSError):
             return False
         if not torch.cuda.is_available():
             return False
-        return bool(lib.trinix_attn_is_available())
+        ok = bool(lib.trinix_attn_is_available())
+        TritonAttentionKernel._available = ok
+        return ok
 
     @staticmethod
     def _prepare_mask(attn_mask: torch.Tensor, batch_size: int, num_heads: int,
@@ -209,11 +217,100 @@ class TritonAttentionKernel:
         return out
 
 
+# ---------------------------------------------------------------------------
+# Launch cache.  A call without mask, ALiBi, dropout, q-norm or lse output
+# whose operands the kernels read in place is described, apart from its data
+# pointers, by its tensors' shapes, strides, dtypes and devices and its
+# scalar arguments.  The first such call goes through the full path below
+# (checks, operand preparation, the argument struct) and leaves a template
+# of its launch here; later calls of the same layout copy the template, set
+# the pointers and launch.  A call that would not pass every check never
+# leaves a template, so the errors of the full path are unchanged.
+# ---------------------------------------------------------------------------
+class _Launch:
+    __slots__ = ("args", "out_shape", "dtype", "device", "align", "rope", "split")
+
+    def __init__(self, args, out_shape, dtype, device, align, rope, split):
+        self.args = args            # AttnFwdArgs with null data pointers
+        self.out_shape = out_shape
+        self.dtype = dtype
+        self.device = device
+        self.align = align          # byte alignment the operand pointers need
+        self.rope = rope            # k pre-pass: (k_stride, out_stride, B, S, H, D, cs_stride, rows) or None
+        self.split = split          # split-KV workspace bytes, or None for trinix_attn_fwd
+
+
+_LAUNCHES: dict = {}
+_MAX_LAUNCHES = 256
+
+
+def _launch_key(q, k, v, causal, scale, window_size, rotary_cos, rotary_sin, rotary_k):
+    """Everything a cached launch depends on except the data pointers, or
+    None when an argument is not hashable."""
+    try:
+        rk = None
+        if rotary_cos is not None:
+            if rotary_sin is None:
+                return None
+            rk = (rotary_cos.shape, rotary_cos.stride(), rotary_cos.dtype, rotary_cos.device, rotary_sin.shape,
+                  rotary_sin.stride(), rotary_sin.dtype, rotary_sin.device, bool(rotary_k))
+        key = (q.shape, q.stride(), q.dtype, q.device, k.shape, k.stride(), k.dtype, k.device, v.shape, v.stride(),
+               v.dtype, v.device, bool(causal), scale, None if window_size is None else tuple(window_size), rk,
+               SPLITKV_ENABLED)
+        hash(key)
+        return key
+    except (TypeError, AttributeError):
+        return None
+
+
+def _launch_cached(key, q, k, v, rotary_cos, rotary_sin):
+    """The output of a call whose layout has a cached launch, or None."""
+    ent = _LAUNCHES.get(key)
+    if ent is None:
+        return None
+    qp, kp, vp = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    if ent.rope is not None:
+        cp, sp = rotary_cos.data_ptr(), rotary_sin.data_ptr()
+        if (qp | kp | vp | cp | sp) % ent.align:
+            return None
+    elif (qp | kp | vp) % ent.align:
+        return None
+    lib = nat.load_library()
+    stream = current_stream_ptr(ent.device)
+    a = nat.AttnFwdArgs.from_buffer_copy(ent.args)
+    if ent.rope is not None:
+        ks, os_, B, S, H, D, cs_stride, rows = ent.rope
+        kr = torch.empty((B, S, H, D), dtype=ent.dtype, device=ent.device)
+        nat.check(lib.trinix_rope_apply(kp, ks, kr.data_ptr(), os_, B, S, H, D, a.dtype, cp, sp, cs_stride, rows,
+                                        None, stream), "trinix_rope_apply")
+        kp = kr.data_ptr()
+        a.rope_cos, a.rope_sin = cp, sp
+    out = torch.empty(ent.out_shape, dtype=ent.dtype, device=ent.device)
+    a.q, a.k, a.v, a.out = qp, kp, vp, out.data_ptr()
+    if ent.split is None:
+        nat.check(lib.trinix_attn_fwd(ctypes.byref(a), stream), "trinix_attn_fwd")
+    else:
+        ws = torch.empty(ent.split, dtype=torch.uint8, device=ent.device) if ent.split else None
+        nat.check(lib.trinix_attn_fwd_splitkv(ctypes.byref(a), None if ws is None else ws.data_ptr(), ent.split,
+                                              stream), "trinix_attn_fwd_splitkv")
+    return out
+
+
 def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, rotary_cos, rotary_sin,
              rotary_k, return_lse, use_blockmap, keep_state=False, q_norm_weight=None, q_norm_eps=1e-6):
     """Launch ``trinix_attn_fwd``; returns (out, lse or None, state).  With
     ``keep_state`` the prepared operands (padded, strided as the kernel reads
     them), the lse and the mask / slope tensors are kept for the backward."""
+    key = None
+    if (attn_mask is None and alibi_slopes is None and not dropout_p and q_norm_weight is None and not return_lse
+            and not keep_state):
+        key = _launch_key(q, k, v, causal, scale, window_size, rotary_cos, rotary_sin, rotary_k)
+        if key is not None:
+            out = _launch_cached(key, q, k, v, rotary_cos, rotary_sin)
+            if out is not None:
+                return out, None, None
+    q_in, k_in, v_in, cos_in, sin_in = q, k, v, rotary_cos, rotary_sin
+    rope_tpl = None
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
         raise ValueError("TritonAttentionKernel requires GPU tensors")
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -256,7 +353,8 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
         if rotary_cos.shape[0] < max(Sq, Sk) or rotary_cos.shape[-1] < D // 2:
             raise ValueError("rotary tables are smaller than (seq_len, head_dim/2)")
         if rotary_k:
-            from .rope_kernel import rope_apply
+            from .rope_kernel import rope_apply, rope_template
+            rope_tpl = rope_template(k, rotary_cos, rotary_sin) if key is not None else None
             k = rope_apply(k, rotary_cos, rotary_sin)
         if d_kernel != D:
             # RoPE pairs (d, d + D/2) of the unpadded head dim: rotate q
@@ -361,6 +459,7 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
         args.q_norm_weight, args.q_norm_eps = qw.data_ptr(), float(q_norm_eps)
 
     launched = False
+    split_bytes = None
     if split_kv:
         ns, wsb = ctypes.c_int32(0), ctypes.c_int64(0)
         rc = lib.trinix_attn_fwd_splitkv_plan(ctypes.byref(args), ctypes.byref(ns), ctypes.byref(wsb))
@@ -371,9 +470,25 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
                                              stream)
             nat.check(rc, "trinix_attn_fwd_splitkv")
             launched = True
+            split_bytes = wsb.value
     if not launched:
         rc = lib.trinix_attn_fwd(ctypes.byref(args), stream)
         nat.check(rc, "trinix_attn_fwd")
+    if key is not None and d_kernel == D:
+        # the operands went to the kernel as given (no copy, no padding, q
+        # not rotated ahead, tables used in place): remember the launch
+        in_place = qk is q_in and vk is v_in and (kk is k_in if rope_tpl is None else True)
+        if rotary_cos is not None or cos_in is not None:
+            in_place = (in_place and rotary_cos is cos_in and args.rope_cos == cos_in.data_ptr()
+                        and args.rope_sin == sin_in.data_ptr() and
+                        (not rotary_k or (rope_tpl is not None and rope_tpl[-1])))
+        if in_place:
+            tpl = nat.AttnFwdArgs.from_buffer_copy(args)
+            tpl.q = tpl.k = tpl.v = tpl.out = tpl.rope_cos = tpl.rope_sin = None
+            if len(_LAUNCHES) >= _MAX_LAUNCHES:
+                _LAUNCHES.clear()
+            _LAUNCHES[key] = _Launch(tpl, tuple(out.shape), q.dtype, device, 16 if q.element_size() == 2 else 4,
+                                     rope_tpl[:-1] if rope_tpl is not None else None, split_bytes)
     state = None
     if keep_state:
         state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),

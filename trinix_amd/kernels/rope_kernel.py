@@ -81,6 +81,21 @@ def rope_apply(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     return out
 
 
+def rope_template(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """The arguments ``rope_apply(x, cos, sin)`` passes to
+    ``trinix_rope_apply`` apart from its data pointers: (x strides, out
+    strides, B, S, H, D, table row stride, table rows, in_place), where
+    in_place says that x and the tables are read as given (no copy, no
+    conversion), which a cached launch needs."""
+    B, S, H, D = x.shape
+    c, s = _table(cos, x), _table(sin, x)
+    in_place = (x.stride(-1) == 1 and c is cos and s is sin and c.stride(0) == s.stride(0) and c.dim() == 2
+                and c.shape[-1] >= D // 2 and c.shape[0] >= S)
+    out_stride = (S * H * D, H * D, D, 1)
+    return ((ctypes.c_int64 * 4)(*x.stride()), (ctypes.c_int64 * 4)(*out_stride), B, S, H, D, c.stride(0),
+            c.shape[0], in_place)
+
+
 class _RoPEFunction(torch.autograd.Function):
     """RoPE of one tensor; the backward is the rotation by -theta."""
 
