@@ -44,6 +44,9 @@ def parse():
                     help="time the workload only: no MALL-flushed, forward+backward, decode or layer fields "
                          "(for profiler runs)")
     ap.add_argument("--all", action="store_true", help="also time every other workload (extra field)")
+    ap.add_argument("--counters", action="store_true",
+                    help="for counter-collection profiler runs: W warm-up and K timed steps only (no clock "
+                         "warm-up, no kernel timing blocks); prints the step time only")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (scale factor of the HBM byte counters)")
     return ap.parse_args()
@@ -433,6 +436,22 @@ def main():
 
     w = WORKLOADS[args.workload]
     dname = DTYPE_NAME[str(w.dtype)]
+    if args.counters:
+        # each dispatch is serialised and its counters read out: keep the
+        # run to a handful of dispatches of the step's kernels
+        from trinix_amd.workloads import make_inputs
+        inp = make_inputs(w, device="cuda")
+        fn = step_fn(w, inp, torch)
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        print(json.dumps({"workload": w.name, "counters_run": True,
+                          "ms_per_step": round((time.perf_counter() - t0) * 1e3 / args.steps, 4)}), flush=True)
+        return
     inp, fl, ms, kms, cold_ms, _, step_gpu, nblk = measure(w, args, torch, cold=not args.no_extra)
     value = fl / (ms * 1e-3) / 1e12
     k_tflops = fl / (kms * 1e-3) / 1e12
