@@ -50,6 +50,9 @@
  *                                 trinix/kernels/utils.py:87-153
  *   trinix_attn_is_available   <- TritonAttentionKernel.is_available
  *                                 trinix/kernels/attention_kernel.py:470-477
+ *   trinix_dropout_state_advance <- no counterpart: the generator state torch keeps for
+ *                                 the eager path's F.dropout under graph capture
+ *                                 (trinix/layers/attention/base.py:395)
  */
 #ifndef TRINIX_ATTN_H
 #define TRINIX_ATTN_H
@@ -60,7 +63,7 @@
 extern "C" {
 #endif
 
-#define TRINIX_ATTN_ABI_VERSION 4
+#define TRINIX_ATTN_ABI_VERSION 5
 
 typedef enum trinix_status {
   TRINIX_OK = 0,
@@ -139,6 +142,12 @@ typedef struct trinix_attn_fwd_args {
    * with a mask or dropout (TRINIX_ERR_BAD_ARGUMENT); NULL = none. */
   const void* q_norm_weight;
   float q_norm_eps;
+  /* Dropout seed and offset in device memory (ABI version 5): two uint64,
+   * {seed, offset}, 8-byte aligned, read by the kernels when they run in
+   * place of dropout_seed / dropout_offset, so that a HIP graph replay can
+   * draw new keep masks (trinix_dropout_state_advance writes them inside the
+   * graph).  NULL = use dropout_seed / dropout_offset. */
+  const uint64_t* dropout_state;
 } trinix_attn_fwd_args;
 
 /* Attention forward on `stream`. */
@@ -330,6 +339,7 @@ typedef struct trinix_attn_bwd_args {
   float dropout_p;              /* the forward's dropout_p, seed and offset */
   uint64_t dropout_seed;
   uint64_t dropout_offset;
+  const uint64_t* dropout_state; /* the forward's, as in trinix_attn_fwd_args */
 } trinix_attn_bwd_args;
 int trinix_attn_bwd(const trinix_attn_bwd_args* args, void* stream);
 
@@ -355,6 +365,16 @@ int trinix_attn_is_available(void);
 
 /* Static description of a status code. */
 const char* trinix_status_string(int status);
+
+/* Dropout under HIP graph capture: no counterpart in the reference, whose
+ * eager dropout (trinix/layers/attention/base.py:395, F.dropout) takes its
+ * seed and offset from torch's graph-safe generator state.  Copies
+ * generator[0..1] = {seed, offset} to call_state[0..1] and advances
+ * generator[1] by `increment`, in one single-lane kernel on `stream`: a
+ * call captured in a graph then draws a new offset on every replay, and the
+ * forward and backward of that call read the same call_state.  Both
+ * pointers are device memory, 8-byte aligned, two uint64 each. */
+int trinix_dropout_state_advance(uint64_t* generator, uint64_t* call_state, uint64_t increment, void* stream);
 
 /* TRINIX_ATTN_ABI_VERSION of the built library. */
 int trinix_abi_version(void);

@@ -102,6 +102,7 @@ def _args(**kw):
     (dict(v_stride=nat.int64x4((1 << 30, 1 << 22, 128, 1))), nat.TRINIX_ERR_BAD_STRIDE),
     (dict(dropout_p=1.0), nat.TRINIX_ERR_BAD_ARGUMENT),
     (dict(mask_blockmap=4096), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(dropout_p=0.1, dropout_state=4100), nat.TRINIX_ERR_BAD_ARGUMENT),  # {seed, offset}: 8-byte aligned
     # mask strides are non-negative, and the 32 rows of a query sub-tile sit
     # at 32-bit offsets from its first row: min(Sq - 1, 31) * row stride < 2^31
     (dict(mask=4096, mask_dtype=nat.TRINIX_F32, mask_stride=nat.int64x4((0, 0, -64, 1))), nat.TRINIX_ERR_BAD_STRIDE),

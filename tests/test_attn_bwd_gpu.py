@@ -457,13 +457,17 @@ def test_layer_training_step_head_dim_256():
     _check_layer(grads, 2e-3)
 
 
-def test_dropout_refused_under_graph_capture(monkeypatch):
-    """Under capture the host-drawn seed would be frozen into the graph (every
-    replay dropping the same elements): the call raises instead.  The
-    capture state is faked, so no graph is captured."""
+def test_dropout_under_capture_needs_the_device_generator(monkeypatch):
+    """A call with dropout under capture reads the device's dropout generator,
+    which only a call outside a capture can create (its seed is copied to
+    the device): without one the call raises before launching anything.
+    The capture state is faked, so no graph is captured."""
+    import trinix_amd.kernels.attention_kernel as ak
+
     q = torch.randn(1, 64, 2, 64, device=DEV, dtype=torch.bfloat16)
+    monkeypatch.setattr(ak, "_DROPOUT_GENERATORS", {})
     monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
-    with pytest.raises(RuntimeError, match="graph"):
+    with pytest.raises(RuntimeError, match="dropout generator"):
         triton_attn_func(q, q, q, dropout_p=0.1)
     triton_attn_func(q, q, q, dropout_p=0.0)  # without dropout the call proceeds
 

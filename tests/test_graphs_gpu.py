@@ -150,3 +150,92 @@ def test_graph_forward_backward():
         torch.cuda.synchronize()
         for name, a, b in zip(("out", "dq", "dk", "dv"), replayed, ref):
             assert torch.equal(a, b), f"replay {rnd}: {name} differs from eager"
+
+
+def test_dropout_state_advance_through_the_abi():
+    """trinix_dropout_state_advance copies the generator {seed, offset} to the
+    call's state and advances the generator's offset, on the stream."""
+    import ctypes
+
+    from trinix_amd import _native as nat
+    from trinix_amd.kernels.attention_kernel import current_stream_ptr
+
+    lib = nat.load_library()
+    gen = torch.tensor([(1 << 62) + 12345, (7 << 32) + 5], dtype=torch.int64, device=DEV)
+    call = torch.full((2,), -1, dtype=torch.int64, device=DEV)
+    st = current_stream_ptr(gen.device)
+    for n in range(3):
+        assert lib.trinix_dropout_state_advance(gen.data_ptr(), call.data_ptr(), ctypes.c_uint64(3), st) == 0
+        torch.cuda.synchronize()
+        assert call.tolist() == [(1 << 62) + 12345, (7 << 32) + 5 + 3 * n]
+        assert gen.tolist() == [(1 << 62) + 12345, (7 << 32) + 5 + 3 * (n + 1)]
+    assert lib.trinix_dropout_state_advance(None, call.data_ptr(), 1, st) == nat.TRINIX_ERR_NULL_POINTER
+    assert lib.trinix_dropout_state_advance(gen.data_ptr() + 4, call.data_ptr(), 1, st) == nat.TRINIX_ERR_BAD_ARGUMENT
+
+
+def _max_err_rule(h, e, t, small):
+    scale = t.abs().max().item()
+    err_h, err_e = (h - t).abs().max().item(), (e - t).abs().max().item()
+    return err_h <= 2 * err_e + small * scale, (err_h, err_e, scale)
+
+
+@pytest.mark.parametrize("dtype,D,kw", [(torch.bfloat16, 128, dict(causal=True)),
+                                        (torch.float16, 64, dict(window_size=(40, 10))),
+                                        (torch.float32, 64, dict(causal=True))])
+def test_graph_training_step_with_dropout_draws_a_new_mask_per_replay(dtype, D, kw):
+    """A captured forward + backward with attention dropout.  A kernel of the
+    graph copies the device's dropout generator to the call's {seed, offset}
+    and advances it, so each replay drops a different set of weights; each
+    replay's output and gradients are those of eager autograd of the oracle
+    through the keep mask of that replay's {seed, offset} (the fp64 answer
+    within twice the eager error in the same dtype)."""
+    from oracle import attention_oracle as orc
+    import trinix_amd.kernels.attention_kernel as ak
+
+    B, S, H, HKV, p = 1, 112, 4, 2, 0.25
+    g0 = torch.Generator().manual_seed(91)
+    q0, k0, v0 = (torch.randn(B, S, h, D, generator=g0) for h in (H, HKV, HKV))
+    do0 = torch.randn(B, S, H, D, generator=g0)
+    q, k, v = (t.to(DEV, dtype).requires_grad_(True) for t in (q0, k0, v0))
+    do = do0.to(DEV, dtype)
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = triton_attn_func(q, k, v, dropout_p=p, **kw)
+        out.backward(do)
+        return out
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    q.grad = k.grad = v.grad = None
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = triton_attn_func(q, k, v, dropout_p=p, **kw)
+        out.backward(do)
+    gen = ak._DROPOUT_GENERATORS[q.device]
+    small = 1e-5 if dtype == torch.float32 else 2e-3
+    keeps = []
+    for rnd in range(3):
+        seed, off = (int(x) for x in gen.tolist())
+        graph.replay()
+        _ = torch.randn(64, 64, device=DEV) @ torch.randn(64, 64, device=DEV)  # eager work between replays
+        torch.cuda.synchronize()
+        assert int(gen.tolist()[1]) == off + 1
+        keep = torch.from_numpy(orc.dropout_keep(B, H, S, S, p, seed, off))
+        keeps.append(keep)
+        res = {}
+        for name, dt in (("truth", torch.float64), ("eager", dtype)):
+            ts = [t.detach().to(dt).clone().requires_grad_(True) for t in (q0, k0, v0)]
+            o = orc.functional_attention(*ts, keep=keep, dropout_p=p, **kw)
+            o.backward(do0.to(dt))
+            res[name] = [o.detach().double()] + [t.grad.double() for t in ts]
+        hip = [out.detach().cpu().double()] + [t.grad.cpu().double() for t in (q, k, v)]
+        for name, h, e, t in zip(("out", "dq", "dk", "dv"), hip, res["eager"], res["truth"]):
+            ok, info = _max_err_rule(h, e, t, small)
+            assert ok, (rnd, name, info)
+    assert not torch.equal(keeps[0], keeps[1]) and not torch.equal(keeps[1], keeps[2])

@@ -120,6 +120,7 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.seed_hi = (uint32_t)(a->dropout_seed >> 32);
   p.off_lo = (uint32_t)a->dropout_offset;
   p.off_hi = (uint32_t)(a->dropout_offset >> 32);
+  p.drop_state = a->dropout_state;
   const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0);
 
   hipStream_t st = (hipStream_t)stream;

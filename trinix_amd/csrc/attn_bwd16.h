@@ -65,6 +65,7 @@ struct BwdParams {
   uint32_t drop_thresh;  // dropped when the 16-bit Philox field < drop_thresh
   float drop_scale;      // 1 / (1 - p)
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
+  const uint64_t* drop_state;  // {seed, offset} in device memory, read in place of the four above; or null
 };
 
 // Allowed (i, j): j - i in [dlo, dhi] (causal: j <= i; window: -wl <= j-i <= wr).
@@ -168,16 +169,16 @@ __device__ inline uint32_t gather_keep_bits(uint32_t own, int e8, std::integer_s
 // consecutive keys), so the eight lanes share every call: lane e8 makes the
 // calls of rows v = e8 and e8 + 8 (one call per 8 elements, as in the
 // forward) and the group hands out the keep bytes through DPP (bcast8).
-__device__ inline uint32_t keep_bits_of_key(const BwdParams& p, int bh, int j, int r0) {
+__device__ inline uint32_t keep_bits_of_key(const DropKey& dkey, int bh, int j, int r0) {
   const int e8 = j & 7;
   uint32_t own = 0;  // bit 8h + k: row r(e8 + 8h), key 8*(j/8) + k
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int v = e8 + 8 * h;
-    const u32x4_t c = {(uint32_t)(j >> 3), (uint32_t)(r0 + (v >> 2) * 8 + (v & 3)), (uint32_t)bh, p.off_lo};
-    const u32x4_t w = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+    const u32x4_t c = {(uint32_t)(j >> 3), (uint32_t)(r0 + (v >> 2) * 8 + (v & 3)), (uint32_t)bh, dkey.off_lo};
+    const u32x4_t w = Philox::run(c, dkey.k0, dkey.k1);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) own |= (keep_field(w[k >> 1], k & 1, p.drop_thresh) ? 1u : 0u) << (8 * h + k);
+    for (int k = 0; k < 8; ++k) own |= (keep_field(w[k >> 1], k & 1, dkey.thresh) ? 1u : 0u) << (8 * h + k);
   }
   // rows v = q and q + 8 come from lane q of the group
   return gather_keep_bits(own, e8, std::make_integer_sequence<int, 8>{});
@@ -214,6 +215,8 @@ __device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, bool DROP>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
+  DropKey dkey{};
+  if constexpr (DROP) dkey = drop_key(p);
   constexpr int NW = 8, NG = NW / 2, BK = NG * 32, BQ = 64, NSL = 3, NST = BQ / 32;
   constexpr int DS = D / 16, DB = D / 32, UPR = D / 8, TILE = BQ * D;
   constexpr int LPW = BQ * UPR / (64 * NW);  // 16-byte copies per wavefront per Q (or dO) tile
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         }
         if constexpr (DROP) {
           // dV takes the dropped, rescaled P of the forward's PV product
-          const uint32_t km = keep_bits_of_key(p, b * p.Hq + hq, j, i0 + st * 32 + g * 4);
+          const uint32_t km = keep_bits_of_key(dkey, b * p.Hq + hq, j, i0 + st * 32 + g * 4);
           *m_slot(PS, st) = km;
 #pragma unroll
           for (int v = 0; v < 16; ++v) x[v] = __uint_as_float(__float_as_uint(x[v]) & keep_word(km, v));
@@ -595,6 +598,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, bool DROP, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
+  DropKey dkey{};
+  if constexpr (DROP) dkey = drop_key(p);
   constexpr int BM = NW * 32;
   constexpr int DS = D / 16, DB = D / 32, NB = BN / 32, UPR = D / 8;
   constexpr int LPW = BN * UPR / (64 * NW);
@@ -759,12 +764,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
           for (int vq = 0; vq < 4; ++vq) {
             const u32x4_t c = {(uint32_t)((n0 + nb * 32 + vq * 8) >> 3), (uint32_t)i, (uint32_t)(b * p.Hq + hq),
-                               p.off_lo};
-            const u32x4_t w = Philox::run(c, p.seed_lo ^ p.off_hi, p.seed_hi);
+                               dkey.off_lo};
+            const u32x4_t w = Philox::run(c, dkey.k0, dkey.k1);
             const uint32_t w0 = g ? w[2] : w[0], w1 = g ? w[3] : w[1];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const float dpk = keep_field(e < 2 ? w0 : w1, e & 1, p.drop_thresh) ? dp[vq * 4 + e] : 0.f;
+              const float dpk = keep_field(e < 2 ? w0 : w1, e & 1, dkey.thresh) ? dp[vq * 4 + e] : 0.f;
               z[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - lse2) * (dpk - dlt);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -774,13 +779,13 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
           for (int vp = 0; vp < 2; ++vp) {  // 8-key groups vq = 2vp, 2vp + 1: one call per lane pair
             uint32_t wq[2][2];
             philox_pair_words((uint32_t)((n0 + nb * 32 + vp * 16) >> 3), (uint32_t)i, (uint32_t)(b * p.Hq + hq),
-                              p.off_lo, p.seed_lo ^ p.off_hi, p.seed_hi, g, wq[0], wq[1]);
+                              dkey.off_lo, dkey.k0, dkey.k1, g, wq[0], wq[1]);
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 const int v = (vp * 2 + h) * 4 + e;
-                const float dpk = keep_field(wq[h][e >> 1], e & 1, p.drop_thresh) ? dp[v] : 0.f;
+                const float dpk = keep_field(wq[h][e >> 1], e & 1, dkey.thresh) ? dp[v] : 0.f;
                 z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dpk - dlt);
               }
           }

@@ -68,13 +68,12 @@ constexpr int kSP = 33;  // pitch of the 32x32 score tiles in LDS
 // dO.V products dp, P = exp2(s*c + bias - lse2) where (i, j) is allowed;
 // s becomes Pd = P * keep / (1 - p) and dp becomes dZ.  A row whose lse is
 // -inf (no allowed key: the forward wrote NaN) gets zero gradients.
-__device__ inline void grad_group(const BwdParams& p, const Band& band, int bh, int i, int j, float lse2,
-                                  float delta, float slope_l2, const char* mrow, float (&s)[4], float (&dp)[4]) {
+__device__ inline void grad_group(const BwdParams& p, const DropKey& dkey, const Band& band, int bh, int i, int j,
+                                  float lse2, float delta, float slope_l2, const char* mrow, float (&s)[4],
+                                  float (&dp)[4]) {
   // keys j..j+3 are fields (j % 8) + e of the call of their 8-key group
   u32x4_t rr = {0u, 0u, 0u, 0u};
-  if (p.use_dropout)
-    rr = Philox::run((u32x4_t){(uint32_t)(j >> 3), (uint32_t)i, (uint32_t)bh, p.off_lo}, p.seed_lo ^ p.off_hi,
-                     p.seed_hi);
+  if (p.use_dropout) rr = Philox::run((u32x4_t){(uint32_t)(j >> 3), (uint32_t)i, (uint32_t)bh, dkey.off_lo}, dkey.k0, dkey.k1);
   const bool row_ok = i < p.Sq && lse2 != -INFINITY;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -85,7 +84,7 @@ __device__ inline void grad_group(const BwdParams& p, const Band& band, int bh, 
     if (p.mask && ok) z += load_mask_elem(mrow, p.mask_dtype, (int64_t)jj * p.mk_sj) * kLog2e;
     const float pr = ok ? exp2f(z) : 0.f;
     const int kf = (j & 7) + e;
-    const float keep = p.use_dropout ? (keep_field(rr[kf >> 1], kf & 1, p.drop_thresh) ? p.drop_scale : 0.f) : 1.f;
+    const float keep = p.use_dropout ? (keep_field(rr[kf >> 1], kf & 1, dkey.thresh) ? p.drop_scale : 0.f) : 1.f;
     s[e] = pr * keep;
     dp[e] = pr * (dp[e] * keep - delta);
   }
@@ -121,6 +120,7 @@ __global__ __launch_bounds__(256) void bwd_delta_generic(const BwdParams p, int6
 
 template <class T, int D>
 __global__ __launch_bounds__(D, 1) void bwd_dkdv_generic(const BwdParams p) {
+  const DropKey dkey = p.use_dropout ? drop_key(p) : DropKey{};
   constexpr int NW = D / 64, P1 = D + 1, NGRP = kBT * kBT / 4 / D;
   __shared__ float lq[kBT * P1];
   __shared__ float ldo[kBT * P1];
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(D, 1) void bwd_dkdv_generic(const BwdParams p) {
             pv[e] = c;
           }
           const int i = i0 + q;
-          grad_group(p, band, b * p.Hq + hq, i, j0 + kq, llse[q], ldel[q], slope_l2, mask_row(p, b, hq, i), sv, pv);
+          grad_group(p, dkey, band, b * p.Hq + hq, i, j0 + kq, llse[q], ldel[q], slope_l2, mask_row(p, b, hq, i), sv, pv);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             lpd[q * kSP + kq + e] = sv[e];
@@ -258,6 +258,7 @@ __global__ __launch_bounds__(D, 1) void bwd_dkdv_generic(const BwdParams p) {
 
 template <class T, int D>
 __global__ __launch_bounds__(D, 1) void bwd_dq_generic(const BwdParams p) {
+  const DropKey dkey = p.use_dropout ? drop_key(p) : DropKey{};
   constexpr int NW = D / 64, P1 = D + 1, NGRP = kBT * kBT / 4 / D;
   __shared__ float lk[kBT * P1];
   __shared__ float lv[kBT * P1];
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(D, 1) void bwd_dq_generic(const BwdParams p) {
           pv[e] = c;
         }
         const int i = i0 + q;
-        grad_group(p, band, b * p.Hq + hq, i, jt + kq, llse[q], ldel[q], slope_l2, mask_row(p, b, hq, i), sv, pv);
+        grad_group(p, dkey, band, b * p.Hq + hq, i, jt + kq, llse[q], ldel[q], slope_l2, mask_row(p, b, hq, i), sv, pv);
 #pragma unroll
         for (int e = 0; e < 4; ++e) ldz[q * kSP + kq + e] = pv[e];
       }

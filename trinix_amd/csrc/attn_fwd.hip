@@ -86,6 +86,7 @@ __device__ inline int classify_tile(const FwdParams& p, int b, int hq, int iw0, 
 
 template <int D, int NW>
 __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
+  const DropKey dkey = p.use_dropout ? drop_key(p) : DropKey{};
   constexpr int NT = NW * 64;
   constexpr int BM = NW * 32;
   constexpr int BN = 32;
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(NW * 64, 1) void attn_fwd_f32(const FwdParams p) {
           xa[e] = s[vp * 8 + e];
           xb[e] = s[vp * 8 + 4 + e];
         }
-        dropout_pair(xa, xb, p, b * p.Hq + hq, i, n0 + vp * 16, g);
+        dropout_pair(xa, xb, dkey, b * p.Hq + hq, i, n0 + vp * 16, g);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           s[vp * 8 + e] = xa[e];
@@ -394,6 +395,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.seed_hi = (uint32_t)(a->dropout_seed >> 32);
   p.off_lo = (uint32_t)a->dropout_offset;
   p.off_hi = (uint32_t)(a->dropout_offset >> 32);
+  p.drop_state = a->dropout_state;
   p.rope_cos = (const uint16_t*)a->rope_cos;
   p.rope_sin = (const uint16_t*)a->rope_sin;
   p.rope_stride = a->rope_stride;

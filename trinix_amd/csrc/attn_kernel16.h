@@ -268,6 +268,8 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
   if (jhi < jlo) jlo = INT_MAX;  // no allowed key: (j - jlo) wraps past jspan for every j
   float slope_l2 = 0.f;
   if constexpr (ALIBI) slope_l2 = -p.alibi[b * p.al_sb + hq * p.al_sh] * kLog2e;
+  DropKey dkey{};
+  if constexpr (DROP) dkey = drop_key(p);
   // ALiBi is folded into the score accumulator: S^T starts at bias / c
   // instead of 0, so s * c = q.k * c + bias and the softmax of a full tile is
   // the plain one (raw max, one FMA before the exp).
@@ -565,7 +567,7 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
             xa[e] = s[nb][vp * 8 + e];
             xb[e] = s[nb][vp * 8 + 4 + e];
           }
-          dropout_pair(xa, xb, p, b * p.Hq + hq, i, n0 + nb * 32 + vp * 16, g);
+          dropout_pair(xa, xb, dkey, b * p.Hq + hq, i, n0 + nb * 32 + vp * 16, g);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             s[nb][vp * 8 + e] = xa[e];

@@ -34,6 +34,7 @@ struct FwdParams {
   uint32_t drop_thresh;  // drop when the 16-bit Philox field < drop_thresh
   float drop_scale;      // 1 / (1 - p)
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
+  const uint64_t* drop_state;  // {seed, offset} in device memory, read in place of the four above; or null
   const uint16_t* rope_cos;
   const uint16_t* rope_sin;
   int64_t rope_stride;
@@ -84,18 +85,39 @@ __device__ inline void load_mask4(const void* base, int dtype, int j0, int64_t s
   }
 }
 
+// The dropout stream of one launch (common.h keep_field): Philox key
+// (seed_lo ^ offset_hi, seed_hi), counter word 3 = offset_lo, and the keep
+// threshold.  The seed and offset are the launch arguments, or, when the
+// caller passes dropout_state, the two uint64 there, read once at the start
+// of the kernel (a HIP graph replay then runs with the values a preceding
+// trinix_dropout_state_advance wrote).
+struct DropKey {
+  uint32_t k0, k1, off_lo, thresh;
+};
+template <class P>
+__device__ inline DropKey drop_key(const P& p) {
+  uint32_t slo = p.seed_lo, shi = p.seed_hi, olo = p.off_lo, ohi = p.off_hi;
+  if (p.drop_state) {
+    const uint64_t s = p.drop_state[0], o = p.drop_state[1];
+    slo = (uint32_t)s;
+    shi = (uint32_t)(s >> 32);
+    olo = (uint32_t)o;
+    ohi = (uint32_t)(o >> 32);
+  }
+  return DropKey{slo ^ ohi, shi, olo, p.drop_thresh};
+}
+
 // Dropout (common.h keep_field) on keys ga + 4g + e (xa) and ga + 8 + 4g + e
 // (xb), e = 0..3, of row i, ga % 8 == 0, g the lane half (the lane pair
 // l, l + 32 holds row i): p <- keep ? p : 0.  The 1/(1-p) of the kept
 // weights is applied to the output once, in the kernels' epilogues.
-__device__ inline void dropout_pair(float (&xa)[4], float (&xb)[4], const FwdParams& p, int bh, int i, int ga, int g) {
+__device__ inline void dropout_pair(float (&xa)[4], float (&xb)[4], const DropKey& dkey, int bh, int i, int ga, int g) {
   uint32_t wa[2], wb[2];
-  philox_pair_words((uint32_t)(ga >> 3), (uint32_t)i, (uint32_t)bh, p.off_lo, p.seed_lo ^ p.off_hi, p.seed_hi, g, wa,
-                    wb);
+  philox_pair_words((uint32_t)(ga >> 3), (uint32_t)i, (uint32_t)bh, dkey.off_lo, dkey.k0, dkey.k1, g, wa, wb);
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    xa[e] = keep_field(wa[e >> 1], e & 1, p.drop_thresh) ? xa[e] : 0.f;
-    xb[e] = keep_field(wb[e >> 1], e & 1, p.drop_thresh) ? xb[e] : 0.f;
+    xa[e] = keep_field(wa[e >> 1], e & 1, dkey.thresh) ? xa[e] : 0.f;
+    xb[e] = keep_field(wb[e >> 1], e & 1, dkey.thresh) ? xb[e] : 0.f;
   }
 }
 

@@ -183,6 +183,7 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (a->mask_blockmap && !a->mask) return TRINIX_ERR_BAD_ARGUMENT;
   if (a->mask && !mask_strides_ok(a->mask_stride, a->seqlen_q, a->seqlen_k)) return TRINIX_ERR_BAD_STRIDE;
   if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->dropout_state && ((uintptr_t)a->dropout_state & 7)) return TRINIX_ERR_BAD_ARGUMENT;
   if ((a->rope_cos == nullptr) != (a->rope_sin == nullptr)) return TRINIX_ERR_NULL_POINTER;
   if (a->rope_cos && esize == 2 &&
       (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
@@ -202,6 +203,7 @@ int validate_bwd_args(const trinix_attn_bwd_args* a) {
   if (a->dtype != TRINIX_F16 && a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F32) return TRINIX_ERR_BAD_DTYPE;
   if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
   if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->dropout_state && ((uintptr_t)a->dropout_state & 7)) return TRINIX_ERR_BAD_ARGUMENT;
   if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0 ||
       a->nheads_q % a->nheads_kv != 0)
     return TRINIX_ERR_BAD_SHAPE;

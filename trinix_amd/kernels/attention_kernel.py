@@ -217,6 +217,24 @@ class TritonAttentionKernel:
         return out
 
 
+# Per device: the dropout generator {seed, offset} (two int64 in device
+# memory) that calls captured in a HIP graph draw from.  Created by the
+# first call with dropout outside a capture, seeded from torch's initial
+# seed (torch.manual_seed makes it reproducible; no draw from torch's
+# generator, so the eager calls' seeds are unchanged), offsets from 2^32 up
+# so that its streams never repeat an eager call's (offset 0).
+_DROPOUT_GENERATORS: dict = {}
+
+
+def dropout_generator(device: torch.device) -> torch.Tensor:
+    gen = _DROPOUT_GENERATORS.get(device)
+    if gen is None:
+        seed = (torch.initial_seed() * 0x9E3779B97F4A7C15 + 0x632BE59BD9B4E019) % (1 << 63)
+        gen = torch.tensor([seed, 1 << 32], dtype=torch.int64, device=device)
+        _DROPOUT_GENERATORS[device] = gen
+    return gen
+
+
 # ---------------------------------------------------------------------------
 # Launch cache.  A call without mask, ALiBi, dropout, q-norm or lse output
 # whose operands the kernels read in place is described, apart from its data
@@ -428,16 +446,30 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             args.mask_blockmap = bmap.data_ptr()
             args.blockmap_stride = nat.int64x2(bst)
 
+    drop_state = None
     if dropout_p > 0.0:
-        if torch.cuda.is_current_stream_capturing():
-            # the seed becomes a kernel argument: every replay would drop
-            # the same elements
-            raise RuntimeError("attention dropout cannot be captured in a HIP graph (the seed would be frozen); "
-                               "capture with dropout_p=0")
-        # Seed from torch's CPU generator: no device->host sync.
         args.dropout_p = float(dropout_p)
-        args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
-        args.dropout_offset = 0
+        if torch.cuda.is_current_stream_capturing():
+            # A seed passed as a kernel argument would be frozen into the
+            # graph.  Instead a kernel of the graph copies the device's
+            # generator {seed, offset} to this call's own state and advances
+            # the generator, and the kernels of this call (forward and
+            # backward) read that state: every replay draws a new mask.
+            gen = _DROPOUT_GENERATORS.get(device)
+            if gen is None:
+                raise RuntimeError(
+                    "attention dropout under HIP graph capture reads the device's dropout generator, which one "
+                    "call with dropout_p > 0 outside the capture creates (the warm-up before capturing)")
+            drop_state = torch.empty(2, dtype=torch.int64, device=device)
+            nat.check(lib.trinix_dropout_state_advance(gen.data_ptr(), drop_state.data_ptr(), 1, stream),
+                      "trinix_dropout_state_advance")
+            args.dropout_state = drop_state.data_ptr()
+            keep.append(drop_state)
+        else:
+            dropout_generator(device)
+            # Seed from torch's CPU generator: no device->host sync.
+            args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+            args.dropout_offset = 0
 
     if rotary_cos is not None:
         cos = rotary_cos.to(device=device, dtype=q.dtype)
@@ -493,7 +525,8 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
     if keep_state:
         state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),
                      window=window_size, D=D, d_kernel=d_kernel, keep=keep, args=args,
-                     dropout=(float(args.dropout_p), int(args.dropout_seed), int(args.dropout_offset)))
+                     dropout=(float(args.dropout_p), int(args.dropout_seed), int(args.dropout_offset)),
+                     dropout_state=drop_state)
     if d_kernel != D:
         out = out[..., :D].contiguous()
     return out, lse, state
@@ -528,6 +561,8 @@ def _backward(state, dout):
     a.mask, a.mask_dtype, a.mask_stride = fa.mask, fa.mask_dtype, fa.mask_stride
     a.mask_blockmap, a.blockmap_stride = fa.mask_blockmap, fa.blockmap_stride
     a.dropout_p, a.dropout_seed, a.dropout_offset = state["dropout"]
+    if state["dropout_state"] is not None:
+        a.dropout_state = state["dropout_state"].data_ptr()
     rc = nat.load_library().trinix_attn_bwd(ctypes.byref(a), current_stream_ptr(qk.device))
     nat.check(rc, "trinix_attn_bwd")
     if dkrn != D:
