@@ -4,8 +4,12 @@
 // UndefinedBehaviorSanitizer (every report fatal).  It runs the status-code
 // cases of the C ABI's validation, then a seeded fuzz over the whole range of
 // every size, stride and window field (int64 extremes included), and checks
-// the split-KV plan's invariants on every accepted decode call.  Exit status
-// 0 and a final "ok" line mean no sanitizer report and no failed check.
+// the split-KV plan's invariants on every accepted decode call.  The bounds
+// model (bounds_model.h) then walks the kernels' index maps for the
+// BASELINE configurations and edge shapes (every work item and row where
+// the grid is small enough) and for a share of the accepted fuzz cases.
+// Exit status 0 and a final "ok" line mean no sanitizer report and no
+// failed check.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -13,6 +17,7 @@
 #include <cstring>
 #include <limits>
 
+#include "bounds_model.h"
 #include "host_plan.h"
 
 using namespace trinix;
@@ -288,6 +293,112 @@ int main() {
     if (pick_dq_wide(a.head_dim, a.batch, a.nheads_q, a.seqlen_q, a.causal || a.has_window, masked))
       CHECK(a.head_dim == 128 && !masked, "wide dQ only at head_dim 128 without a mask");
   }
+  // ---- bounds model: curated shapes (every item and row where small), then
+  // a share of the fuzz's accepted argument sets (sampled items)
+  bounds::Report BR;
+  int modelled = 0;
+  auto model_one = [&](const trinix_attn_fwd_args& f, int64_t limit) {
+    if (validate_fwd_args(&f) != TRINIX_OK || f.dtype == TRINIX_F32) return;
+    FwdPlan fp;
+    if (plan_fwd(&f, &fp) == TRINIX_OK) bounds::model_fwd16(BR, f, fp, limit);
+    SplitPlan sp;
+    if (make_split_plan(&f, &sp)) bounds::model_decode(BR, f, sp, limit);
+    if (f.head_dim <= 128 && f.q_norm_weight == nullptr) {
+      trinix_attn_bwd_args b = valid_bwd();
+      b.batch = f.batch, b.seqlen_q = f.seqlen_q, b.seqlen_k = f.seqlen_k, b.nheads_q = f.nheads_q;
+      b.nheads_kv = f.nheads_kv, b.head_dim = f.head_dim, b.dtype = f.dtype, b.causal = f.causal;
+      b.has_window = f.has_window, b.window_left = f.window_left, b.window_right = f.window_right;
+      b.mask = f.mask, b.mask_dtype = f.mask_dtype, b.mask_blockmap = f.mask_blockmap, b.dropout_p = f.dropout_p;
+      for (int i = 0; i < 4; ++i) {
+        b.q_stride[i] = b.dout_stride[i] = b.out_stride[i] = b.dq_stride[i] = f.q_stride[i];
+        b.k_stride[i] = b.dk_stride[i] = f.k_stride[i];
+        b.v_stride[i] = b.dv_stride[i] = f.v_stride[i];
+        b.mask_stride[i] = f.mask_stride[i];
+      }
+      BwdPlan bp;
+      if (validate_bwd_args(&b) == TRINIX_OK && plan_bwd(&b, &bp) == TRINIX_OK) bounds::model_bwd16(BR, b, bp, limit);
+    }
+    ++modelled;
+  };
+  auto shape = [](int64_t B, int64_t Sq, int64_t Sk, int64_t Hq, int64_t Hkv, int64_t D, int dtype) {
+    trinix_attn_fwd_args a = valid_fwd();
+    a.batch = B, a.seqlen_q = Sq, a.seqlen_k = Sk, a.nheads_q = Hq, a.nheads_kv = Hkv, a.head_dim = D, a.dtype = dtype;
+    const int64_t q[4] = {Sq * Hq * D, Hq * D, D, 1}, kv[4] = {Sk * Hkv * D, Hkv * D, D, 1};
+    for (int i = 0; i < 4; ++i) a.q_stride[i] = a.out_stride[i] = q[i], a.k_stride[i] = a.v_stride[i] = kv[i];
+    return a;
+  };
+  {
+    const int64_t kAll = 1 << 16;  // list every work item / row up to this many
+    std::vector<trinix_attn_fwd_args> cur;
+    auto add = [&](trinix_attn_fwd_args a) { cur.push_back(a); };
+    trinix_attn_fwd_args a;
+    a = shape(4, 1024, 1024, 12, 12, 64, TRINIX_BF16), a.causal = 1, add(a);          // C2
+    a = shape(1, 8192, 8192, 32, 8, 128, TRINIX_BF16), a.causal = 1, add(a);          // C3
+    a = shape(2, 16384, 16384, 32, 8, 128, TRINIX_BF16), a.causal = 1;                // C4
+    a.has_window = 1, a.window_left = 4096, a.window_right = 0, add(a);
+    a = shape(8, 2048, 2048, 16, 16, 64, TRINIX_F16);                                 // C5a, mask + block map
+    a.mask = (void*)4096, a.mask_dtype = TRINIX_F32, a.mask_blockmap = (const uint8_t*)4096;
+    a.mask_stride[0] = a.mask_stride[1] = 0, a.mask_stride[2] = 2048, a.mask_stride[3] = 1, add(a);
+    a.nheads_kv = 1, a.k_stride[2] = a.v_stride[2] = 0, add(a);                       // C5b (expanded KV)
+    for (int64_t D : {64, 128, 256})
+      for (int64_t Sq : {1, 17, 100, 128, 300})
+        for (int64_t Sk : {1, 63, 64, 65, 300})
+          for (int c = 0; c < 6; ++c) {
+            a = shape(2, Sq, Sk, 4, c % 2 ? 1 : 2, D, c % 3 ? TRINIX_BF16 : TRINIX_F16);
+            a.causal = c & 1;
+            if (c >= 2) a.has_window = 1, a.window_left = c == 4 ? -3 : 40, a.window_right = c == 5 ? (1ll << 62) : 7;
+            if (c == 3) a.mask = (void*)4096, a.mask_dtype = TRINIX_BF16, a.mask_blockmap = (const uint8_t*)4096,
+                        a.mask_stride[2] = Sk, a.mask_stride[3] = 1;
+            if (c == 5) a.dropout_p = 0.25f;
+            add(a);
+          }
+    a = shape(1, 40000, 40000, 2, 1, 64, TRINIX_BF16), a.causal = 1, a.has_window = 1;  // long, two-sided window
+    a.window_left = 8192, a.window_right = 300, add(a);
+    a = shape(3, 9, 70000, 32, 8, 128, TRINIX_BF16), a.causal = 1, add(a);              // decode shapes
+    a = shape(16, 1, 8192, 32, 8, 128, TRINIX_BF16), add(a);
+    a = shape(1, 5, 777, 8, 2, 64, TRINIX_F16), a.has_window = 1, a.window_left = 100, a.window_right = -2, add(a);
+    a = shape(1, 64, 64, 8, 8, 128, TRINIX_BF16), a.has_window = 1;                       // extreme windows
+    a.window_left = std::numeric_limits<int64_t>::min(), a.window_right = std::numeric_limits<int64_t>::max(), add(a);
+    a.window_left = std::numeric_limits<int64_t>::max(), a.window_right = std::numeric_limits<int64_t>::min(), add(a);
+    for (const auto& f : cur) model_one(f, kAll);
+    cases += (int)cur.size();
+  }
+  {
+    // fuzz share: 1 in 40 accepted 16-bit argument sets, sampled items
+    bounds::g_sample_ends = 3, bounds::g_sample_inner = 6;
+    rng = 0x1234567887654321ull;
+    int ran = 0;
+    for (int it = 0; it < 400000 && ran < 1500; ++it) {
+      trinix_attn_fwd_args a = valid_fwd();
+      a.batch = next_u64() % 3 ? (int64_t)(1 + next_u64() % 8) : rand_size();
+      a.seqlen_q = next_u64() % 2 ? (int64_t)(1 + next_u64() % 20) : rand_size();
+      a.seqlen_k = rand_size();
+      a.nheads_kv = (int64_t)(1 + next_u64() % 8);
+      a.nheads_q = a.nheads_kv * (int64_t)(1 + next_u64() % 8);
+      a.head_dim = (int64_t)(64 << (next_u64() % 3));
+      a.dtype = next_u64() % 2 ? TRINIX_BF16 : TRINIX_F16;
+      a.causal = (int32_t)(next_u64() % 2);
+      a.has_window = (int32_t)(next_u64() % 2);
+      a.window_left = rand_size();
+      a.window_right = rand_size();
+      if (next_u64() % 2) a.window_left = (int64_t)(next_u64() % 3000) - 1000;  // small, both signs
+      if (next_u64() % 2) a.window_right = (int64_t)(next_u64() % 3000) - 1000;
+      const int64_t kvs = next_u64() % 2 ? a.nheads_kv * a.head_dim : (int64_t)(8 * (next_u64() % (1 << 19)));
+      a.k_stride[1] = a.v_stride[1] = kvs;
+      if (next_u64() % 3 == 0) {
+        a.mask = (void*)4096, a.mask_dtype = (int32_t)(next_u64() % 4);
+        a.mask_blockmap = next_u64() % 2 ? (const uint8_t*)4096 : nullptr;
+        a.mask_stride[0] = rand_size(), a.mask_stride[1] = rand_size();
+        a.mask_stride[2] = rand_size(), a.mask_stride[3] = next_u64() % 2 ? 1 : rand_size();
+      }
+      if (validate_fwd_args(&a) != TRINIX_OK) continue;
+      model_one(a, 4096);
+      ++ran;
+    }
+    cases += ran;
+  }
+  std::printf("bounds model: %d argument sets, %ld checks, %ld failures\n", modelled, BR.checks, BR.failures);
+  failures += (int)BR.failures;
   std::printf("cases %d, fuzz accepted %d, planned %d, failures %d\n", cases, accepted, planned, failures);
   if (failures) return 1;
   std::printf("ok\n");

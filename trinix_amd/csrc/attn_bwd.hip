@@ -91,8 +91,8 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.scale_log2 = a->softmax_scale * kLog2e;
   p.causal = a->causal ? 1 : 0;
   p.has_window = a->has_window ? 1 : 0;
-  p.wl = a->window_left;
-  p.wr = a->window_right;
+  p.wl = clamp_window(a->window_left);
+  p.wr = clamp_window(a->window_right);
   p.alibi = a->alibi_slopes;
   p.al_sb = a->alibi_stride[0];
   p.al_sh = a->alibi_stride[1];
@@ -103,12 +103,12 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.bm_sb = a->blockmap_stride[0];
   p.bm_sh = a->blockmap_stride[1];
   p.bm_cols = (int)((a->seqlen_k + 63) / 64);
-  p.num_kblk = (int)((a->seqlen_k + 127) / 128);
-  p.dq_wide = a->dtype != TRINIX_F32 && pick_dq_wide(a->head_dim, a->batch, a->nheads_q, a->seqlen_q,
-                                                      a->causal || a->has_window, a->mask != nullptr) ? 1 : 0;
-  p.num_mblk = (int)((a->seqlen_q + (p.dq_wide ? 255 : 127)) / (p.dq_wide ? 256 : 128));
-  if ((int64_t)p.B * p.Hq * p.num_mblk >= (1ll << 31) || (int64_t)p.B * p.Hkv * p.num_kblk >= (1ll << 31))
-    return TRINIX_ERR_BAD_SHAPE;
+  BwdPlan plan;
+  const int prc = plan_bwd(a, &plan);
+  if (prc != TRINIX_OK) return prc;
+  p.num_kblk = plan.num_kblk;
+  p.num_mblk = plan.num_mblk;
+  p.dq_wide = plan.dq_wide ? 1 : 0;
   p.use_dropout = a->dropout_p > 0.f ? 1 : 0;
   {
     // dropped when the key's 16-bit Philox field < floor(p * 2^16)

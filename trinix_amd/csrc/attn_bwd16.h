@@ -71,16 +71,7 @@ struct BwdParams {
 // Allowed (i, j): j - i in [dlo, dhi] (causal: j <= i; window: -wl <= j-i <= wr).
 struct Band {
   int dlo, dhi;
-  __device__ Band(const BwdParams& p) {
-    int64_t lo = INT_MIN / 2, hi = INT_MAX / 2;
-    if (p.causal) hi = 0;
-    if (p.has_window) {
-      lo = lo > -p.wl ? lo : -p.wl;
-      hi = hi < p.wr ? hi : p.wr;
-    }
-    dlo = (int)(lo < INT_MIN / 2 ? INT_MIN / 2 : lo);
-    dhi = (int)(hi > INT_MAX / 2 ? INT_MAX / 2 : hi);
-  }
+  __device__ Band(const BwdParams& p) { band_offsets(p.causal != 0, p.has_window != 0, p.wl, p.wr, dlo, dhi); }
   __device__ bool ok(int i, int j) const { return j - i >= dlo && j - i <= dhi; }
 };
 
@@ -235,11 +226,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   const int kg = wave % NG;
   const int g = lane >> 5;
 
-  int w = xcd_remap(blockIdx.x, p.B * p.Hkv * p.num_kblk);
-  const int kblk = w % p.num_kblk;  // causal: low key blocks see the most queries, and run first
-  w /= p.num_kblk;
-  const int hkv = w % p.Hkv;
-  const int b = w / p.Hkv;
+  const KvItem wi = bwd_kv_item((int)blockIdx.x, p.B, p.Hkv, p.num_kblk);  // (index_map.h)
+  const int kblk = wi.kblk, hkv = wi.hkv, b = wi.b;
   const int kb0 = kblk * BK;
   const int j0 = kb0 + kg * 32;
   const int j = j0 + (lane & 31);
@@ -251,16 +239,13 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   const float c = p.scale_log2;
 
   // Query range of the workgroup's keys [kb0, kb0 + BK): i - j in [-dhi, -dlo].
-  const int kmax = min(kb0 + BK, p.Sk) - 1;
-  const int i_lo = (int)max((int64_t)0, (int64_t)kb0 - band.dhi);
-  const int i_hi = (int)min((int64_t)p.Sq, (int64_t)kmax - band.dlo + 1);
-  const int qt_lo = i_lo / BQ;
-  const int qt_hi = i_hi > i_lo ? (i_hi + BQ - 1) / BQ : qt_lo;
+  int qt_lo, qt_hi;
+  bwd_query_tiles(kb0, BK, p.Sq, p.Sk, band.dlo, band.dhi, BQ, qt_lo, qt_hi);
   const int nqt = qt_hi - qt_lo;
   const int n_items = nqt > 0 ? p.G * nqt : 0;  // item = (q-head of the group, query tile)
 
   // ---- tile copies: Q and dO rows (16-byte units, swizzled), lse and delta
-  auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
+  auto ld_row = [&](int l) __attribute__((always_inline)) { return tile_copy_row(wave, LPW, l, lane, UPR); };
   auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_kt<D>(ld_row(l)); };
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
   auto load_rows = [&](const uint16_t* base, int64_t ss, uint16_t* lds_tile, int i0) __attribute__((always_inline)) {
@@ -270,7 +255,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 #pragma unroll
     for (int l = 0; l < LPW; ++l) {
       const uint32_t row = (uint32_t)min(ld_row(l), last);
-      dma_16b_s(row * (uint32_t)ss * 2u + (uint32_t)ld_unit(l) * 16u, gb,
+      dma_16b_s(tile_copy_offset(row, ss, (uint32_t)ld_unit(l)), gb,
                 __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
     }
   };
@@ -613,16 +598,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, g = lane >> 5;
 
-  int w = xcd_remap(blockIdx.x, p.B * p.Hq * p.num_mblk);
-  const int gq = w % p.G;
-  w /= p.G;
-  const int mi = w % p.num_mblk;
-  w /= p.num_mblk;
-  const int hkv = w % p.Hkv;
-  const int b = w / p.Hkv;
+  // (index_map.h; causal: longest rows first)
+  const DqItem wi = bwd_dq_item((int)blockIdx.x, p.B, p.Hq, p.Hkv, p.G, p.num_mblk, p.causal != 0, BM);
+  const int gq = wi.gq, hkv = wi.hkv, b = wi.b, m0 = wi.m0;
   const int hq = hkv * p.G + gq;
-  const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
-  const int m0 = mblk * BM;
   const int iw0 = m0 + wave * 32;
   const int i = iw0 + r;
   const int ic = min(i, p.Sq - 1);
@@ -659,15 +638,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
   for (int db = 0; db < DB; ++db) acc[db] = (f32x16_t){};
 
   // key tiles of the band of rows [m0, m0 + BM): j - i in [dlo, dhi]
-  const int mlast = min(m0 + BM, p.Sq) - 1;
-  const int64_t lo = max((int64_t)0, (int64_t)m0 + band.dlo);
-  const int64_t hi = min((int64_t)p.Sk, (int64_t)mlast + band.dhi + 1);
-  const int t_lo = (int)(lo / BN);
-  const int t_hi = hi > lo ? (int)((hi + BN - 1) / BN) : t_lo;
+  int t_lo, t_hi;
+  bwd_key_tiles(m0, BM, p.Sq, p.Sk, band.dlo, band.dhi, BN, t_lo, t_hi);
 
   const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
+  auto ld_row = [&](int l) __attribute__((always_inline)) { return tile_copy_row(wave, LPW, l, lane, UPR); };
   auto ld_unit = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_kt<D>(ld_row(l)); };
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
   auto load_rows = [&](const uint16_t* base, int64_t ss, uint16_t* lds_tile, int tile) __attribute__((always_inline)) {
@@ -678,7 +654,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
     for (int l = 0; l < LPW; ++l) {
       const uint32_t row = (uint32_t)min(ld_row(l), last);
-      dma_16b_s(row * (uint32_t)ss * 2u + (uint32_t)ld_unit(l) * 16u, gb,
+      dma_16b_s(tile_copy_offset(row, ss, (uint32_t)ld_unit(l)), gb,
                 __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
     }
   };

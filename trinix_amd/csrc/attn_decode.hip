@@ -74,11 +74,8 @@ __global__ __launch_bounds__(256) void attn_decode16(DecParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, lr = lane & 15, lg = lane >> 4;
 
-  int bid = blockIdx.x;
-  const int rg = bid % p.RG;
-  bid /= p.RG;
-  const int split = bid % p.n_splits;
-  const int bh = bid / p.n_splits;
+  const DecItem wi = dec_item((int)blockIdx.x, p.RG, p.n_splits);  // (index_map.h)
+  const int rg = wi.rg, split = wi.split, bh = wi.bh;
   const int b = bh / p.Hkv, kvh = bh % p.Hkv;
 
   // This lane's row (column lr of every score tile).
@@ -87,8 +84,8 @@ __global__ __launch_bounds__(256) void attn_decode16(DecParams p) {
   const int i = row_ok ? r / p.G : 0;
   const int hq = kvh * p.G + (row_ok ? r % p.G : 0);
 
-  const int c0 = p.klo + split * p.chunk;
-  const int c1 = min(p.khi, c0 + p.chunk);
+  int c0, c1;
+  dec_chunk(p.klo, p.khi, p.chunk, split, c0, c1);
 
   // Allowed keys of row i within this chunk: [jlo, jhi].
   int jlo, jhi;
@@ -277,7 +274,7 @@ __global__ __launch_bounds__(256) void attn_decode16(DecParams p) {
     }
     if (p.lse && (tid & 15) == 0) p.lse[((int64_t)b * p.Hq + hq2) * p.Sq + i2] = (mmax + __log2f(L)) * kLn2;
   } else {
-    const int64_t idx = ((int64_t)bh * p.M + r2) * p.n_splits + split;
+    const int64_t idx = dec_partial_index(bh, p.M, r2, p.n_splits, split);
     const float inv = L > 0.f ? 1.f / L : 0.f;
     float* dst = p.part_o + idx * D + dc;
 #pragma unroll
@@ -426,9 +423,8 @@ int launch_splitkv(const trinix_attn_fwd_args* a, const SplitPlan& pl, void* wor
   p.scale_log2 = a->softmax_scale * kLog2e;
   p.causal = a->causal ? 1 : 0;
   p.has_window = a->has_window ? 1 : 0;
-  const int64_t lim = 1ll << 40;
-  p.wl = a->window_left < -lim ? -lim : (a->window_left > lim ? lim : a->window_left);
-  p.wr = a->window_right < -lim ? -lim : (a->window_right > lim ? lim : a->window_right);
+  p.wl = clamp_window(a->window_left);
+  p.wr = clamp_window(a->window_right);
   p.alibi = a->alibi_slopes;
   p.al_sb = a->alibi_stride[0];
   p.al_sh = a->alibi_stride[1];

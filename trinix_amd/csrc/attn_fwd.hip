@@ -267,7 +267,6 @@ using namespace trinix;
 
 namespace {
 
-constexpr int kWavesF32 = 4;
 
 }  // namespace
 
@@ -351,29 +350,18 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.Hkv = (int)a->nheads_kv;
   p.G = p.Hq / p.Hkv;
   const bool f32 = a->dtype == TRINIX_F32;
-  const bool plain = !a->mask && !(a->dropout_p > 0.f);
-  const bool split_ok = plain && a->causal && !a->has_window && !a->q_norm_weight;
-  Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q, a->causal || a->has_window, plain,
-                         split_ok);
-  if (a->q_norm_weight) cfg.ks = 1;  // the fused q RMSNorm is built without the key split
-  if (cfg.ks == 0) {                 // per-item key split: the item table, or no split
-    const int n = split_ok ? plan_split_rows(a->seqlen_q, a->seqlen_k, a->batch * a->nheads_q, 32 * cfg.nw, cfg.bn,
-                                                p.row_items, kMaxRowItems) : 0;
-    if (n > (a->seqlen_q + 32 * cfg.nw - 1) / (32 * cfg.nw)) p.num_mblk = n;
-    else cfg.ks = 1;  // no block split (or no plan): the plain shape, without the per-item decode
-  }
-  if (f32 || cfg.ks != 0) {
-    const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw / cfg.ks;
-    p.num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
-  }
-  const int64_t total = (int64_t)p.B * p.Hq * p.num_mblk;
-  if (total >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
-  p.total_work = (int)total;
+  FwdPlan plan;
+  const int prc = plan_fwd(a, &plan);
+  if (prc != TRINIX_OK) return prc;
+  const Cfg16 cfg = plan.cfg;
+  p.num_mblk = plan.num_mblk;
+  for (int k = 0; k < plan.n_items; ++k) p.row_items[k] = plan.row_items[k];
+  p.total_work = (int)plan.total_work;
   p.scale_log2 = a->softmax_scale * kLog2e;
   p.causal = a->causal ? 1 : 0;
   p.has_window = a->has_window ? 1 : 0;
-  p.wl = a->window_left;
-  p.wr = a->window_right;
+  p.wl = clamp_window(a->window_left);
+  p.wr = clamp_window(a->window_right);
   p.alibi = a->alibi_slopes;
   p.al_sb = a->alibi_stride[0];
   p.al_sh = a->alibi_stride[1];

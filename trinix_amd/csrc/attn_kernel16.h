@@ -95,37 +95,13 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
   // the head groups of an XCD (when the groups split evenly over the 8 XCDs):
   // the long chains then start first and run alone on their CUs, and the
   // short blocks fill in behind them.
-  int gq, mi, hkv, b;
-  const int groups = p.B * p.Hkv;
-  if (p.causal && groups % kXcds == 0) {
-    const int xcd = (int)blockIdx.x % kXcds, j = (int)blockIdx.x / kXcds;  // j: dispatch order in the XCD
-    const int ng = groups / kXcds;
-    mi = j / (ng * p.G);
-    const int rest = j % (ng * p.G);
-    const int hg = xcd * ng + rest / p.G;
-    gq = rest % p.G;
-    hkv = hg % p.Hkv;
-    b = hg / p.Hkv;
-  } else {
-    int w = xcd_remap(blockIdx.x, p.total_work);
-    gq = w % p.G;
-    w /= p.G;
-    mi = w % p.num_mblk;
-    w /= p.num_mblk;
-    hkv = w % p.Hkv;
-    b = w / p.Hkv;
-  }
+  // (index_map.h: fwd_item, fwd_row_block)
+  const FwdItem wi = fwd_item((int)blockIdx.x, p.B, p.Hkv, p.G, p.num_mblk, p.total_work, p.causal != 0);
+  const int gq = wi.gq, mi = wi.mi, hkv = wi.hkv, b = wi.b;
   const int hq = hkv * p.G + gq;
   // ks: wavefronts per 32-row group (1 or 2); bm: rows of the work item
-  int ks = KS, m0;
-  if constexpr (KS == 0) {
-    const uint32_t item = p.row_items[mi];  // row block << 2 | split << 1 | half
-    ks = (item & 2u) ? 2 : 1;
-    m0 = (int)(item >> 2) * (NW * 32) + (int)(item & 1u) * (NW * 16);
-  } else {
-    const int mblk = p.causal ? (p.num_mblk - 1 - mi) : mi;  // longest rows first
-    m0 = mblk * (NW * 32 / KS);
-  }
+  const RowBlock rb = fwd_row_block(KS, NW, mi, p.causal != 0, p.num_mblk, KS == 0 ? (uint32_t)p.row_items[mi] : 0u);
+  const int ks = rb.ks, m0 = rb.m0;
   const int bm = NW * 32 / ks;
   const int kp = wave % ks;  // key parity of this wavefront (key split)
   const int iw0 = m0 + (wave / ks) * 32;
@@ -135,24 +111,8 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
   const bool wave_live = iw0 < p.Sq;
 
   // Key tiles the workgroup visits, and the sub-range of full tiles.
-  const int mlast = min(m0 + bm, p.Sq) - 1;
-  int64_t lo = 0, hi = p.Sk, flo = 0, fhi = p.Sk;
-  if (p.causal) {
-    hi = min(hi, (int64_t)mlast + 1);
-    fhi = min(fhi, (int64_t)m0 + 1);
-  }
-  if (p.has_window) {
-    lo = max(lo, (int64_t)m0 - p.wl);
-    hi = min(hi, (int64_t)mlast + p.wr + 1);
-    flo = max(flo, (int64_t)mlast - p.wl);
-    fhi = min(fhi, (int64_t)m0 + p.wr + 1);
-  }
-  const int t_lo = (int)(lo / BN);
-  const int t_hi = hi > lo ? (int)((hi + BN - 1) / BN) : t_lo;
-  int t_flo = (int)((flo + BN - 1) / BN);
-  int t_fhi = fhi > 0 ? (int)(fhi / BN) : 0;
-  t_flo = min(max(t_flo, t_lo), t_hi);
-  t_fhi = min(max(t_fhi, t_flo), t_hi);
+  const TileRange trange = fwd_tile_range(m0, bm, p.Sq, p.Sk, p.causal != 0, p.has_window != 0, p.wl, p.wr, BN);
+  const int t_lo = trange.t_lo, t_hi = trange.t_hi, t_flo = trange.t_flo, t_fhi = trange.t_fhi;
   // Scores stay in the raw domain, s = q.k (+ bias / c), and the scale
   // c = scale * log2 e > 0 is applied in the FMA before the exp, so the max of
   // the raw scores is the max of the scaled ones.  A negative scale negates
@@ -292,14 +252,14 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
   // -inf and their P is 0, so they never contribute.
   const uint16_t* kbase = p.k + b * p.k_sb + hkv * p.k_sh;
   const uint16_t* vbase = p.v + b * p.v_sb + hkv * p.v_sh;
-  auto ld_row = [&](int l) __attribute__((always_inline)) { return ((wave * LPW + l) * 64 + lane) / UPR; };
+  auto ld_row = [&](int l) __attribute__((always_inline)) { return tile_copy_row(wave, LPW, l, lane, UPR); };
   auto ld_unit_k = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_k<D>(ld_row(l)); };
   auto ld_unit_v = [&](int l) __attribute__((always_inline)) { return (lane % UPR) ^ swz_v<D>(ld_row(l)); };
   uint32_t ld_koff[LPW], ld_voff[LPW];
 #pragma unroll
   for (int l = 0; l < LPW; ++l) {
-    ld_koff[l] = (uint32_t)ld_row(l) * (uint32_t)p.k_ss * 2u + (uint32_t)ld_unit_k(l) * 16u;
-    ld_voff[l] = (uint32_t)ld_row(l) * (uint32_t)p.v_ss * 2u + (uint32_t)ld_unit_v(l) * 16u;
+    ld_koff[l] = tile_copy_offset((uint32_t)ld_row(l), p.k_ss, (uint32_t)ld_unit_k(l));
+    ld_voff[l] = tile_copy_offset((uint32_t)ld_row(l), p.v_ss, (uint32_t)ld_unit_v(l));
   }
   const uint64_t kbase_s = uniform_ptr(kbase), vbase_s = uniform_ptr(vbase);
   const uint32_t wave_lds = __builtin_amdgcn_readfirstlane((uint32_t)(wave * LPW * 1024));
@@ -317,7 +277,7 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
       for (int l = 0; l < LPW; ++l) {
         const uint32_t row = (uint32_t)min(ld_row(l), last);
         const uint32_t unit = (uint32_t)(is_k ? ld_unit_k(l) : ld_unit_v(l));
-        dma_16b_s(row * (uint32_t)ss * 2u + unit * 16u, gb, __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
+        dma_16b_s(tile_copy_offset(row, ss, unit), gb, __builtin_amdgcn_readfirstlane(lds0 + l * 1024));
       }
     }
   };

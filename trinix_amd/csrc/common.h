@@ -9,6 +9,8 @@
 #include <type_traits>
 #include <utility>
 
+#include "index_map.h"
+
 namespace trinix {
 
 // Launches `kernel` on `st` through hipLaunchKernel and returns the status of
@@ -93,17 +95,6 @@ struct F16 {
 // Round an fp32 value to the storage precision of E and back.
 template <class E>
 __device__ inline float round_to(float x) { return E::lo(E::pack(x, 0.f)); }
-
-// Workgroups are dispatched round-robin over the kXcds = 8 XCDs of an
-// MI355X (WG x runs on XCD x % 8).  Give each XCD one contiguous range of the
-// work list, so work items that read the same K/V (neighbouring items) share
-// that XCD's L2.
-constexpr int kXcds = 8;
-__device__ inline int xcd_remap(int x, int total) {
-  const int xcd = x % kXcds, idx = x / kXcds;
-  const int per = total / kXcds, rem = total % kXcds;
-  return xcd * per + (xcd < rem ? xcd : rem) + idx;
-}
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw: "Parallel random numbers: as
 // easy as 1, 2, 3", SC'11), the counter-based generator used for dropout.

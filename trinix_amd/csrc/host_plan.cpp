@@ -224,6 +224,50 @@ int validate_bwd_args(const trinix_attn_bwd_args* a) {
   return TRINIX_OK;
 }
 
+int64_t clamp_window(int64_t w) {
+  const int64_t lim = 1ll << 30;
+  return w < -lim ? -lim : (w > lim ? lim : w);
+}
+
+int plan_fwd(const trinix_attn_fwd_args* a, FwdPlan* pl) {
+  const bool f32 = a->dtype == TRINIX_F32;
+  const bool plain = !a->mask && !(a->dropout_p > 0.f);
+  const bool split_ok = plain && a->causal && !a->has_window && !a->q_norm_weight;
+  Cfg16 cfg = pick_cfg16(a->head_dim, a->batch, a->nheads_q, a->seqlen_q, a->causal || a->has_window, plain,
+                         split_ok);
+  if (a->q_norm_weight) cfg.ks = 1;  // the fused q RMSNorm is built without the key split
+  pl->n_items = 0;
+  pl->num_mblk = 0;
+  if (cfg.ks == 0) {  // per-item key split: the item table, or no split
+    const int n = split_ok ? plan_split_rows(a->seqlen_q, a->seqlen_k, a->batch * a->nheads_q, 32 * cfg.nw, cfg.bn,
+                                             pl->row_items, kMaxRowItems) : 0;
+    if (n > (a->seqlen_q + 32 * cfg.nw - 1) / (32 * cfg.nw)) {
+      pl->num_mblk = n;
+      pl->n_items = n;
+    } else {
+      cfg.ks = 1;  // no block split (or no plan): the plain shape, without the per-item decode
+    }
+  }
+  if (f32 || cfg.ks != 0) {
+    const int bm = f32 ? 32 * kWavesF32 : 32 * cfg.nw / cfg.ks;
+    pl->num_mblk = (int)((a->seqlen_q + bm - 1) / bm);
+  }
+  pl->cfg = cfg;
+  pl->total_work = a->batch * a->nheads_q * pl->num_mblk;
+  if (pl->total_work >= (1ll << 31)) return TRINIX_ERR_BAD_SHAPE;
+  return TRINIX_OK;
+}
+
+int plan_bwd(const trinix_attn_bwd_args* a, BwdPlan* pl) {
+  pl->num_kblk = (int)((a->seqlen_k + 127) / 128);
+  pl->dq_wide = a->dtype != TRINIX_F32 && pick_dq_wide(a->head_dim, a->batch, a->nheads_q, a->seqlen_q,
+                                                       a->causal || a->has_window, a->mask != nullptr);
+  pl->num_mblk = (int)((a->seqlen_q + (pl->dq_wide ? 255 : 127)) / (pl->dq_wide ? 256 : 128));
+  if (a->batch * a->nheads_q * pl->num_mblk >= (1ll << 31) || a->batch * a->nheads_kv * pl->num_kblk >= (1ll << 31))
+    return TRINIX_ERR_BAD_SHAPE;
+  return TRINIX_OK;
+}
+
 bool make_split_plan(const trinix_attn_fwd_args* a, SplitPlan* pl) {
   if (a->dtype != TRINIX_BF16 && a->dtype != TRINIX_F16) return false;
   if (a->dropout_p > 0.f || a->rope_cos || a->q_norm_weight) return false;
@@ -233,9 +277,7 @@ bool make_split_plan(const trinix_attn_fwd_args* a, SplitPlan* pl) {
   const int64_t G = a->nheads_q / a->nheads_kv;
   const int64_t M = G * Sq;
   const int64_t RG = (M + 15) / 16;
-  const int64_t lim = 1ll << 40;
-  const int64_t wl = a->window_left < -lim ? -lim : (a->window_left > lim ? lim : a->window_left);
-  const int64_t wr = a->window_right < -lim ? -lim : (a->window_right > lim ? lim : a->window_right);
+  const int64_t wl = clamp_window(a->window_left), wr = clamp_window(a->window_right);
   // Keys some row i in [0, Sq) may see: lo(i) = max(0, i - wl) is smallest at
   // i = 0, hi(i) = min(Sk - 1, i (causal), i + wr (window)) largest at Sq - 1.
   int64_t klo = a->has_window ? -wl : 0;

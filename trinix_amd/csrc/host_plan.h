@@ -46,6 +46,34 @@ int plan_split_rows(int64_t sq, int64_t sk, int64_t heads, int rows, int bn, uin
 // Whether the 16-bit dQ backward runs 256-row workgroups with 128-key tiles.
 bool pick_dq_wide(int64_t head_dim, int64_t batch, int64_t hq, int64_t sq, bool banded, bool masked);
 
+// Window bounds as the kernels take them: every |j - i| < 2^30 (seqlen_q,
+// seqlen_k < 2^30), so a bound beyond +-2^30 selects the same keys as
+// +-2^30, and the kernels' index arithmetic on it stays in 32 bits.
+int64_t clamp_window(int64_t w);
+
+// Launch plan of trinix_attn_fwd (the 16-bit kernels' tile shape, or the
+// fp32 kernel's): row blocks per (batch, q-head), grid size and the per-item
+// key split table.
+constexpr int kWavesF32 = 4;
+struct FwdPlan {
+  Cfg16 cfg;           // 16-bit kernels; cfg.ks = 0 only with n_items > 0
+  int num_mblk;        // work items per (batch, q-head)
+  int64_t total_work;  // workgroups
+  int n_items;         // entries of row_items (cfg.ks == 0)
+  uint8_t row_items[kMaxRowItems];
+};
+// TRINIX_OK, or TRINIX_ERR_BAD_SHAPE when the grid exceeds 2^31 - 1
+// workgroups.  For validated arguments.
+int plan_fwd(const trinix_attn_fwd_args* a, FwdPlan* pl);
+
+// Launch plan of trinix_attn_bwd's 16-bit kernels: 128-key blocks (dK/dV)
+// and 128- or 256-row blocks (dQ).
+struct BwdPlan {
+  int num_kblk, num_mblk;
+  bool dq_wide;
+};
+int plan_bwd(const trinix_attn_bwd_args* a, BwdPlan* pl);
+
 // Split-KV decode plan.
 constexpr int kDecodeMaxSq = 16;
 constexpr int kDecodeTargetWgs = 1024;  // 4 workgroups of 4 wavefronts per CU

@@ -4,46 +4,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "index_map.h"
+
 namespace trinix {
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
-
-// Swizzle of the 16-byte units of a D-wide row-major tile row.  K rows are
-// read 16 bytes per lane, 16 consecutive rows per access; V rows are read 8
-// bytes per lane by ds_read_b64_tr_b16, 4 consecutive rows x 64 bytes per
-// 32 lanes.  Rows of D >= 128 (256 or 512 bytes) all start on bank 0, so
-// the unit index is XORed with the row (mod 16 units); 128-byte rows (D = 64)
-// pair up first.
-template <int D>
-__device__ inline int swz_k(int row) {
-  return D >= 128 ? (row & 15) : ((row >> 1) & 7);
-}
-template <int D>
-__device__ inline int swz_v(int row) {
-  return D >= 128 ? 4 * (row & 3) : 4 * ((row >> 1) & 1);
-}
-
-// Swizzle of tiles read both ways: row-wise (ds_read_b128, 16 consecutive
-// rows per access phase) and by ds_read_b64_tr_b16 (4 consecutive rows x 64
-// bytes per 32 lanes).  Rows sharing a bank period need distinct units for
-// the row reads (a bijection of the 16 rows onto the 16 units); the
-// transpose reads need the 64-byte group (unit bits 2-3) to differ across
-// any 4 consecutive rows.  Swapping the two 2-bit fields of the row index
-// gives both (for D = 64, two 128-byte rows share a period: the same on
-// (row >> 1) & 7 with fields of 1 and 2 bits).  swz_k alone conflicts 4-way
-// on the transpose reads.
-template <int D>
-__device__ inline int swz_kt(int row) {
-  if constexpr (D >= 128) {
-    const int s = row & 15;
-    return ((s & 3) << 2) | (s >> 2);
-  } else {
-    const int s = (row >> 1) & 7;
-    return ((s & 1) << 2) | (s >> 1);
-  }
-}
 
 // Asynchronous global -> LDS copy (global_load_lds_dwordx4): lane l's 16
 // bytes land at LDS byte address lds_base + 16*l (lds_base wave-uniform).
