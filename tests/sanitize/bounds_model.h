@@ -152,7 +152,7 @@ inline void model_fwd16(Report& R, const trinix_attn_fwd_args& a, const FwdPlan&
   std::vector<uint8_t> seen_item(all ? (size_t)total : 0), seen_row(all ? (size_t)B * Hq * Sq : 0);
   const int64_t bmap_rows = ((int64_t)Sq + 31) / 32, bmap_cols = ((int64_t)Sk + 63) / 64;
   for (int64_t blk : sample(total, all ? total : 0)) {
-    const FwdItem it = fwd_item((int)blk, B, Hkv, G, pl.num_mblk, (int)total, causal);  // attn_kernel16.h:92-100
+    const FwdItem it = fwd_item((int)blk, B, Hkv, G, pl.num_mblk, (int)total, causal, win);
     if (!R.expect(it.b >= 0 && it.b < B && it.hkv >= 0 && it.hkv < Hkv && it.gq >= 0 && it.gq < G && it.mi >= 0 &&
                       it.mi < pl.num_mblk,
                   "fwd item", "block %lld -> out of range (b %lld, hkv %lld, mi %lld)", blk, it.b, it.hkv, it.mi))

@@ -458,6 +458,34 @@ def test_fully_masked_rows_give_nan_like_eager():
     assert_parity(out, ref, torch.float16, "nan rows")
 
 
+@pytest.mark.parametrize("D,dtype", [(64, torch.float16), (128, torch.bfloat16)])
+def test_window_bounds_beyond_the_sequence_are_exact(D, dtype):
+    """Window bounds of any size select the keys they name: (2^40, 0) with
+    causal is causal, (5, 2^62) is (5, Sk), and a bound of -2^40 (no key
+    within reach) gives the NaN rows of an empty softmax, in the forward and
+    the backward.  (Bounds are clamped to +-2^30 ahead of the kernels'
+    32-bit index arithmetic; |j - i| < 2^30 for every accepted shape.)"""
+    B, S, H, HKV = 1, 200, 4, 2
+    q, k, v = rand((B, S, H, D), dtype, 61), rand((B, S, HKV, D), dtype, 62), rand((B, S, HKV, D), dtype, 63)
+    big = 1 << 40
+    assert torch.equal(triton_attn_func(q, k, v, causal=True, window_size=(big, 0)),
+                       triton_attn_func(q, k, v, causal=True))
+    assert torch.equal(triton_attn_func(q, k, v, window_size=(5, 1 << 62)),
+                       triton_attn_func(q, k, v, window_size=(5, S)))
+    assert torch.equal(triton_attn_func(q, k, v, window_size=(S, 1 << 62)),
+                       triton_attn_func(q, k, v, window_size=(1 << 62, S)))
+    out = triton_attn_func(q, k, v, window_size=(-big, big))  # needs j - i >= 2^40: no key
+    assert torch.isnan(out).all()
+    # the backward takes the same band: gradients equal those of the small bounds
+    grads = []
+    for ws in ((big, 3), (S, 3)):
+        ts = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+        triton_attn_func(*ts, causal=True, window_size=ws).backward(torch.ones_like(q))
+        grads.append([t.grad for t in ts])
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
 def test_single_open_column_returns_that_value_row():
     B, S, H, D = 1, 128, 2, 128
     q, k, v = rand((B, S, H, D), torch.bfloat16, 51), rand((B, S, H, D), torch.bfloat16, 52), rand((B, S, H, D), torch.bfloat16, 53)

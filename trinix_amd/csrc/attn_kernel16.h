@@ -96,7 +96,8 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
   // the long chains then start first and run alone on their CUs, and the
   // short blocks fill in behind them.
   // (index_map.h: fwd_item, fwd_row_block)
-  const FwdItem wi = fwd_item((int)blockIdx.x, p.B, p.Hkv, p.G, p.num_mblk, p.total_work, p.causal != 0);
+  const FwdItem wi =
+      fwd_item((int)blockIdx.x, p.B, p.Hkv, p.G, p.num_mblk, p.total_work, p.causal != 0, p.has_window != 0);
   const int gq = wi.gq, mi = wi.mi, hkv = wi.hkv, b = wi.b;
   const int hq = hkv * p.G + gq;
   // ks: wavefronts per 32-row group (1 or 2); bm: rows of the work item

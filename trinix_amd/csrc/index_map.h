@@ -2,7 +2,7 @@
 // which query rows and key tiles it covers, and the offsets of its tile
 // copies.  Plain integer code with no HIP dependency, marked __host__
 // __device__: the kernels inline it, and the CPU bounds model
-// (tests/sanitize/bounds_model.cpp, built by g++ with the two attributes
+// (tests/sanitize/bounds_model.h, built by g++ with the two attributes
 // defined empty) runs the same functions over the launch plans of
 // host_plan.cpp to check every address they produce against the tensors'
 // extents.
@@ -82,20 +82,33 @@ __host__ __device__ inline uint32_t tile_copy_offset(uint32_t row, int64_t ss, u
 // dispatched longest first across all the head groups of an XCD (when the
 // groups split evenly over the 8 XCDs): the long chains then start first
 // and run alone on their CUs, and the short blocks fill in behind them.
+// With a causal window the row blocks have (nearly) one length and each
+// reads a window of K/V: an XCD then runs its head groups one after the
+// other, row blocks longest first within each, so that its resident
+// workgroups read one group's window (C4: 16 groups, two per XCD; with
+// both interleaved the XCD's 4 MB L2 held neither window).
 struct FwdItem {
   int b, hkv, gq, mi;
 };
 __host__ __device__ inline FwdItem fwd_item(int blk, int B, int Hkv, int G, int num_mblk, int total_work,
-                                            bool causal) {
+                                            bool causal, bool windowed) {
   FwdItem it;
   const int groups = B * Hkv;
   if (causal && groups % kXcds == 0) {
     const int xcd = blk % kXcds, j = blk / kXcds;  // j: dispatch order in the XCD
     const int ng = groups / kXcds;
-    it.mi = j / (ng * G);
-    const int rest = j % (ng * G);
-    const int hg = xcd * ng + rest / G;
-    it.gq = rest % G;
+    int hg;
+    if (windowed) {
+      const int per = num_mblk * G;  // one head group's items
+      hg = xcd * ng + j / per;
+      it.mi = (j % per) / G;
+      it.gq = j % G;
+    } else {
+      it.mi = j / (ng * G);
+      const int rest = j % (ng * G);
+      hg = xcd * ng + rest / G;
+      it.gq = rest % G;
+    }
     it.hkv = hg % Hkv;
     it.b = hg / Hkv;
   } else {
@@ -134,7 +147,7 @@ __host__ __device__ inline RowBlock fwd_row_block(int KS, int NW, int mi, bool c
 // Key tiles of BN keys a workgroup of rows [m0, m0 + bm) visits,
 // [t_lo, t_hi), and its full tiles [t_flo, t_fhi) (every (i, j) of the
 // workgroup allowed): causal j <= i, window -wl <= j - i <= wr, j < Sk.
-// wl and wr are at most 2^40 in magnitude (clamped by the host).
+// wl and wr are at most 2^30 in magnitude (clamp_window, host_plan.cpp).
 struct TileRange {
   int t_lo, t_hi, t_flo, t_fhi;
 };
