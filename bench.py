@@ -44,6 +44,9 @@ def parse():
                     help="time the workload only: no MALL-flushed, forward+backward, decode or layer fields "
                          "(for profiler runs)")
     ap.add_argument("--all", action="store_true", help="also time every other workload (extra field)")
+    ap.add_argument("--backward", action="store_true",
+                    help="time forward + backward steps of the workload (its mask, ALiBi, window and RoPE "
+                         "included) instead of the forward; with --counters, only W + K such steps")
     ap.add_argument("--counters", action="store_true",
                     help="for counter-collection profiler runs: W warm-up and K timed steps only (no clock "
                          "warm-up, no kernel timing blocks); prints the step time only")
@@ -173,10 +176,10 @@ def cold_step_ms(fn, torch, iters=10):
     return sorted(times)[len(times) // 2]
 
 
-def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0):
-    """ms of one differentiable step on the workload: forward (with the
-    workload's RoPE) and backward to q, k, v through the HIP kernels, with
-    attention dropout ``dropout_p``."""
+def fwd_bwd_step(w, inp, torch, dropout_p=0.0):
+    """One differentiable step on the workload: forward (with the workload's
+    RoPE, window, ALiBi and mask) and backward to q, k, v through the HIP
+    kernels, with attention dropout ``dropout_p``."""
     from trinix_amd import triton_attn_func
 
     q, k, v = (t.detach().clone().requires_grad_(True) for t in (inp.q, inp.k, inp.v))
@@ -184,13 +187,26 @@ def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0):
     kw = dict(causal=w.causal, window_size=w.window, dropout_p=dropout_p)
     if inp.cos is not None:
         kw.update(rotary_cos=inp.cos, rotary_sin=inp.sin)
+    if inp.mask is not None:
+        kw["attn_mask"] = inp.mask
+    if inp.alibi is not None:
+        kw["alibi_slopes"] = inp.alibi
 
     def step():
         # gradients start from None each step, as after optimizer.zero_grad()
         # (set_to_none=True, its default): no accumulation kernels are timed
         q.grad = k.grad = v.grad = None
-        triton_attn_func(q, k, v, **kw).backward(do)
+        kk, vv = k, v
+        if w.nheads_kv == 1:  # MQA: the layer's stride-0 expand
+            kk, vv = k.expand(-1, -1, w.nheads, -1), v.expand(-1, -1, w.nheads, -1)
+        triton_attn_func(q, kk, vv, **kw).backward(do)
 
+    return step
+
+
+def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0):
+    """ms of one forward + backward step (fwd_bwd_step), host-timed."""
+    step = fwd_bwd_step(w, inp, torch, dropout_p)
     for _ in range(3):
         step()
     torch.cuda.synchronize()
@@ -436,12 +452,21 @@ def main():
 
     w = WORKLOADS[args.workload]
     dname = DTYPE_NAME[str(w.dtype)]
+    if args.backward and not args.counters:
+        from trinix_amd.workloads import make_inputs, flops
+        inp = make_inputs(w, device="cuda")
+        fb = fwd_bwd_ms(w, inp, torch, iters=max(args.steps, 10))
+        fl = flops(w)
+        print(json.dumps({"metric": "attn fwd+bwd TFLOP/s (3.5x the forward's algorithmic flop)", "workload": w.name,
+                          "dtype": dname, "ms_per_step": round(fb, 4), "tflops": round(3.5 * fl / fb / 1e9, 2),
+                          "steps": max(args.steps, 10)}), flush=True)
+        return
     if args.counters:
         # each dispatch is serialised and its counters read out: keep the
         # run to a handful of dispatches of the step's kernels
         from trinix_amd.workloads import make_inputs
         inp = make_inputs(w, device="cuda")
-        fn = step_fn(w, inp, torch)
+        fn = fwd_bwd_step(w, inp, torch) if args.backward else step_fn(w, inp, torch)
         for _ in range(args.warmup):
             fn()
         torch.cuda.synchronize()

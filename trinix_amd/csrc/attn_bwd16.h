@@ -405,11 +405,15 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
           }
         }
         float x[16];
+        // |i - j| = |fj - (row offset in the sub-tile)| with fj = j - (first
+        // row of the lane's group): one subtraction of an immediate and one
+        // FMA per element (the distance is exact in fp32 below 2^24, as
+        // (float)|i - j| is)
+        const float fj = ALIBI ? (float)(j - (i0 + st * 32 + g * 4)) : 0.f;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int i = i0 + st * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
           x[v] = s[v] * c;
-          if constexpr (ALIBI) x[v] += slope_l2 * (float)abs(i - j);
+          if constexpr (ALIBI) x[v] = __builtin_fmaf(fabsf(fj - (float)((v >> 2) * 8 + (v & 3))), slope_l2, x[v]);
         }
         if constexpr (MASK) {
           // rows vq*8 + 4g + 0..3 of the sub-tile: 4 consecutive rows per
