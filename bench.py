@@ -204,17 +204,25 @@ def fwd_bwd_step(w, inp, torch, dropout_p=0.0):
     return step
 
 
-def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0):
-    """ms of one forward + backward step (fwd_bwd_step), host-timed."""
+def fwd_bwd_ms(w, inp, torch, iters=10, dropout_p=0.0, reps=3):
+    """ms of one forward + backward step (fwd_bwd_step), host-timed over
+    `iters` steps bracketed by synchronisations, median of `reps` such loops,
+    after about 0.3 s of warm-up steps (the first loop after a short warm-up
+    read up to 8% slow: clock ramp)."""
     step = fwd_bwd_step(w, inp, torch, dropout_p)
-    for _ in range(3):
+    t_warm, n = time.perf_counter(), 0
+    while n < 3 or time.perf_counter() - t_warm < 0.3:
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        step()
-    torch.cuda.synchronize()
-    return (time.perf_counter() - t0) * 1e3 / iters
+        n += 1
+        torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            step()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3 / iters)
+    return sorted(times)[len(times) // 2]
 
 
 def measure(w, args, torch, cold=False, min_timed_s=0.0, strict=True):

@@ -148,6 +148,12 @@ typedef struct trinix_attn_fwd_args {
    * draw new keep masks (trinix_dropout_state_advance writes them inside the
    * graph).  NULL = use dropout_seed / dropout_offset. */
   const uint64_t* dropout_state;
+  /* With q_norm_weight (ABI version 5): the q the kernel attends with
+   * (after the fused RoPE and RMSNorm) is also written here, a contiguous
+   * (B, Sq, Hq, D) tensor of q's dtype, 16-byte aligned, so that a backward
+   * (trinix_attn_bwd, then trinix_qk_norm_bwd) can use it.  NULL = not
+   * written; requires q_norm_weight. */
+  void* q_norm_out;
 } trinix_attn_fwd_args;
 
 /* Attention forward on `stream`. */

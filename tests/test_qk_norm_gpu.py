@@ -241,6 +241,12 @@ def test_qk_norm_layer_training_uses_fused_kernels(norm_type, monkeypatch):
     x = torch.randn(2, S, E)
     gy = torch.randn(2, S, E)
     grads, outs = [], []
+    from trinix_amd.kernels import attention_kernel as ak
+
+    fused_q_calls = []
+    apply = ak._HipAttnQNormFunction.apply
+    monkeypatch.setattr(ak._HipAttnQNormFunction, "apply",
+                        staticmethod(lambda *a: fused_q_calls.append(1) or apply(*a)))
     for layer, dev, dt in ((ref64, "cpu", torch.float64), (ref16, "cpu", torch.bfloat16), (hip, DEV, torch.bfloat16)):
         if layer is hip:  # the eager norm modules must not run on the fused path
             def refuse(self, x):
@@ -253,6 +259,8 @@ def test_qk_norm_layer_training_uses_fused_kernels(norm_type, monkeypatch):
         outs.append(y.detach().cpu().double())
         grads.append([xi.grad.cpu().double()] + [layer.get_parameter(n).grad.cpu().double() for n in names])
     t, e, h = grads
+    if norm_type == "rmsnorm":  # q's norm ran in the attention prologue, k's in the fused kernel
+        assert fused_q_calls, "the training step did not take the fused q-norm attention"
     assert (outs[2] - outs[0]).abs().max() <= 2 * (outs[1] - outs[0]).abs().max() + 2e-3 * outs[0].abs().max()
     for name, gh, gt, ge in zip(["x"] + names, h, t, e):
         scale = gt.abs().max().item()
@@ -302,6 +310,49 @@ def test_q_norm_fused_into_attention_is_bitwise_the_two_kernel_path(D, dtype, ro
     assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("D,dtype", [(64, torch.float16), (128, torch.bfloat16)])
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("alibi", [False, True])
+def test_q_norm_fused_training_is_bitwise_the_two_kernel_path(D, dtype, rope, alibi, monkeypatch):
+    """Gradients through q's RoPE + RMSNorm fused into the attention
+    prologue: the kernel writes the normalised q it attends with, the
+    attention backward runs on it and the qk-norm backward takes the
+    gradient to the raw q and the norm weight.  Output and every gradient
+    (q, k, v, weight) equal those of qk_rmsnorm, the RoPE of k and the
+    attention as separate differentiable steps, bit for bit."""
+    from trinix_amd.kernels.attention_kernel import attention
+    from trinix_amd.kernels.rope_kernel import rotate
+
+    if D == 64:  # the fused norm is built without the key split: the same kernel on both sides
+        monkeypatch.setenv("TRINIX_ATTN_CFG", "4,2,64,1")
+    g = torch.Generator().manual_seed(D + (3 if rope else 0) + (5 if alibi else 0))
+    B, S, H, HKV = 2, 170, 4, 2
+    q0 = (torch.randn(B, S, H, D, generator=g) * 2).to(DEV, dtype)
+    k0 = torch.randn(B, S, HKV, D, generator=g).to(DEV, dtype)
+    v0 = torch.randn(B, S, HKV, D, generator=g).to(DEV, dtype)
+    w0 = (torch.rand(D, generator=g) + 0.5).to(DEV, dtype)
+    do = torch.randn(B, S, H, D, generator=g).to(DEV, dtype)
+    eps = 1e-5
+    cos = sin = None
+    if rope:
+        cos, sin = _rope_tables(q0, S)
+    slopes = orc.alibi_slopes(H).to(DEV, torch.float32) if alibi else None
+    res = []
+    for fused in (True, False):
+        q, k, v, w = (t.clone().requires_grad_(True) for t in (q0, k0, v0, w0))
+        if fused:
+            out = attention(q, k, v, causal=True, alibi_slopes=slopes, rotary_cos=cos, rotary_sin=sin,
+                            q_norm_weight=w, q_norm_eps=eps)
+        else:
+            qn = qk_rmsnorm(q, w, eps, cos, sin)
+            kr = rotate(k, cos, sin) if rope else k
+            out = attention(qn, kr, v, causal=True, alibi_slopes=slopes)
+        out.backward(do)
+        res.append([out.detach()] + [t.grad for t in (q, k, v, w)])
+    for name, a, b in zip(("out", "dq", "dk", "dv", "dweight"), *res):
+        assert torch.equal(a, b), name
+
+
 def test_q_norm_fused_argument_errors():
     from trinix_amd.kernels import TritonAttentionKernel
     from trinix_amd.kernels.attention_kernel import attention
@@ -316,8 +367,10 @@ def test_q_norm_fused_argument_errors():
     with pytest.raises(ValueError):
         TritonAttentionKernel.apply(q96, q96, q96, q_norm_weight=torch.ones(96, device=DEV, dtype=torch.bfloat16))
     qg = q.clone().requires_grad_(True)
+    with pytest.raises(ValueError):  # differentiable too, but not with a mask or dropout
+        attention(qg, q, q, attn_mask=torch.zeros(32, 32, device=DEV), q_norm_weight=w)
     with pytest.raises(ValueError):
-        attention(qg, q, q, q_norm_weight=w)
+        attention(qg, q, q, dropout_p=0.1, q_norm_weight=w)
     with pytest.raises(ValueError):  # built without the mask and dropout kernels
         TritonAttentionKernel.apply(q, q, q, attn_mask=torch.zeros(32, 32, device=DEV), q_norm_weight=w)
     with pytest.raises(ValueError):

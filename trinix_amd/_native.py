@@ -87,6 +87,7 @@ class AttnFwdArgs(ctypes.Structure):
         ("q_norm_weight", c_void_p),
         ("q_norm_eps", c_float),
         ("dropout_state", c_void_p),
+        ("q_norm_out", c_void_p),
     ]
 
 

@@ -389,6 +389,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.rope_stride = a->rope_stride;
   p.qn_w = (const uint16_t*)a->q_norm_weight;
   p.qn_eps = a->q_norm_eps;
+  p.qn_out = (uint16_t*)a->q_norm_out;
 
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;

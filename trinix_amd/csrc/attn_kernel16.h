@@ -204,6 +204,13 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
         }
         qr[ds] = x;
       }
+      // the q attended with, for a backward (one writer per row: the
+      // fused norm runs without the key split)
+      if (p.qn_out && i < p.Sq) {
+        uint16_t* qo = p.qn_out + (((int64_t)b * p.Sq + i) * p.Hq + hq) * D;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) *(u32x4_t*)(qo + ds * 16 + g * 8) = qr[ds];
+      }
     }
     if (q_neg)
 #pragma unroll

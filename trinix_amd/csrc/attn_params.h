@@ -40,6 +40,7 @@ struct FwdParams {
   int64_t rope_stride;
   const uint16_t* qn_w;  // fused q RMSNorm weight (head_dim), or null
   float qn_eps;
+  uint16_t* qn_out;  // the normalised q, contiguous (B, Sq, Hq, D), or null
   // work items of the per-item key split (Cfg16 ks = 0), longest chain
   // first: row block << 2 | split << 1 | half (plan_split_rows)
   uint8_t row_items[kMaxRowItems];

@@ -188,6 +188,7 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (a->rope_cos && esize == 2 &&
       (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
     return TRINIX_ERR_BAD_STRIDE;
+  if (a->q_norm_out && (!a->q_norm_weight || !aligned16(a->q_norm_out))) return TRINIX_ERR_BAD_ARGUMENT;
   if (a->q_norm_weight) {
     if (esize != 2) return TRINIX_ERR_BAD_DTYPE;
     if (a->mask || a->dropout_p > 0.f) return TRINIX_ERR_BAD_ARGUMENT;

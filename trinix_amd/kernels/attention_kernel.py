@@ -315,7 +315,8 @@ def _launch_cached(key, q, k, v, rotary_cos, rotary_sin):
 
 
 def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, rotary_cos, rotary_sin,
-             rotary_k, return_lse, use_blockmap, keep_state=False, q_norm_weight=None, q_norm_eps=1e-6):
+             rotary_k, return_lse, use_blockmap, keep_state=False, q_norm_weight=None, q_norm_eps=1e-6,
+             q_norm_out=None):
     """Launch ``trinix_attn_fwd``; returns (out, lse or None, state).  With
     ``keep_state`` the prepared operands (padded, strided as the kernel reads
     them), the lse and the mask / slope tensors are kept for the backward."""
@@ -489,6 +490,11 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             qw = qw.contiguous()
         keep.append(qw)
         args.q_norm_weight, args.q_norm_eps = qw.data_ptr(), float(q_norm_eps)
+        if q_norm_out is not None:
+            if (q_norm_out.shape != q.shape or q_norm_out.dtype != q.dtype or not q_norm_out.is_contiguous()
+                    or q_norm_out.data_ptr() % 16):
+                raise ValueError("q_norm_out must be a contiguous, 16-byte aligned tensor shaped and typed like q")
+            args.q_norm_out = q_norm_out.data_ptr()
 
     launched = False
     split_bytes = None
@@ -610,6 +616,52 @@ class _HipAttnFunction(torch.autograd.Function):
         return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
 
 
+class _HipAttnQNormFunction(torch.autograd.Function):
+    """Attention whose q is RoPE-rotated and RMS-normalised in the kernel's
+    prologue (the layers' q_norm, reference grouped_query_attention.py:
+    171-177), with gradients: the forward kernel also writes the normalised
+    q, the attention backward runs on it, and trinix_qk_norm_bwd takes its
+    gradient back through the norm and the RoPE to the raw q and the norm
+    weight.  k is rotated here (rotary_k) and its gradient rotated back."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, weight, eps, causal, scale, window_size, alibi_slopes, rotary_cos, rotary_sin,
+                rotary_k):
+        from .qk_norm_kernel import _param, _rows_ok, _tables
+        from .rope_kernel import rope_apply
+
+        qc = q if _rows_ok(q) else q.contiguous()
+        w = _param(weight)
+        if rotary_cos is not None and rotary_k:
+            k = rope_apply(k, rotary_cos, rotary_sin)
+        qn = torch.empty(qc.shape, dtype=qc.dtype, device=qc.device)
+        out, _, state = _forward(qc, k, v, None, causal, scale, 0.0, window_size, alibi_slopes, rotary_cos,
+                                 rotary_sin, False, True, True, keep_state=True, q_norm_weight=w, q_norm_eps=eps,
+                                 q_norm_out=qn)
+        state["q"] = qn  # the backward's q: the one attended with
+        ctx.state = state
+        c, s, _ = _tables(qc, rotary_cos, rotary_sin, None)
+        ctx.save_for_backward(qc, w, c, s)
+        ctx.eps = float(eps)
+        ctx.rope_k = (rotary_cos, rotary_sin) if rotary_cos is not None and rotary_k else None
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        from .qk_norm_kernel import NORM_RMS
+        from .qk_norm_kernel import _backward as qk_norm_backward
+        from .rope_kernel import rope_apply
+
+        qc, w, c, s = ctx.saved_tensors
+        dqn, dk, dv = _backward(ctx.state, dout.contiguous())
+        ctx.state = None
+        dq, dw, _ = qk_norm_backward(qc, dqn, w, ctx.eps, c, s, None, NORM_RMS)
+        if ctx.rope_k is not None:
+            cos, sin = ctx.rope_k
+            dk = rope_apply(dk, cos, -sin)
+        return dq, dk, dv, dw, None, None, None, None, None, None, None, None
+
+
 def backward_supported(q: torch.Tensor) -> bool:
     """True if ``trinix_attn_bwd`` covers attention on ``q`` (every dtype the
     forward takes, dropout included, at a kernel head_dim)."""
@@ -631,7 +683,18 @@ def attention(q, k, v, attn_mask=None, causal=False, scale=None, dropout_p=0.0, 
     """
     needs_grad = torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v))
     if q_norm_weight is not None and (needs_grad or (torch.is_grad_enabled() and q_norm_weight.requires_grad)):
-        raise ValueError("the fused q RMSNorm has no backward: apply the norm module before attention() to train")
+        # differentiable through the fused q RoPE + RMSNorm (bf16/fp16, no
+        # mask or dropout: the fused norm's own limits, checked by _forward)
+        if attn_mask is not None or dropout_p > 0.0:
+            raise ValueError("the fused q RMSNorm runs without a mask or dropout")
+        if not backward_supported(q):
+            raise ValueError(f"no HIP attention backward for dtype {q.dtype}, head_dim {q.shape[-1]}")
+        if return_lse:
+            raise ValueError("return_lse is not available with a differentiable fused q RMSNorm")
+        if scale is None:
+            scale = q.shape[-1] ** -0.5
+        return _HipAttnQNormFunction.apply(q, k, v, q_norm_weight, q_norm_eps, causal, scale, window_size,
+                                           alibi_slopes, rotary_cos, rotary_sin, rotary_k)
     if needs_grad:
         if not backward_supported(q):
             raise ValueError(f"no HIP attention backward for dtype {q.dtype}, head_dim {q.shape[-1]}")

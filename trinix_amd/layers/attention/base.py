@@ -348,13 +348,13 @@ class FastBaseAttention(nn.Module):
         fuse_norm = self._fused_qk_norm_applies(q, k)
         # q's RoPE + RMSNorm in the attention kernel's prologue (positions are
         # the query rows: no position_ids, no cache, no zero-attention row;
-        # that kernel takes no mask and no dropout, and has no backward
-        # through the norm)
+        # that kernel takes no mask and no dropout).  In training the kernel
+        # also writes the normalised q for the backward, which then runs the
+        # attention backward and the qk-norm backward.
         fuse_qnorm = (self.fuse_q_norm_in_attention and fuse_norm and isinstance(self.q_norm, _QKRMSNorm)
                       and position_ids is None and past_key_value is None
                       and not (use_zero_attn and self.add_zero_attn) and q.shape[-1] in (64, 128, 256)
-                      and attention_mask is None and not (self.training and self.dropout > 0.0)
-                      and not (torch.is_grad_enabled() and (q.requires_grad or self.q_norm.weight.requires_grad)))
+                      and attention_mask is None and not (self.training and self.dropout > 0.0))
         if fuse_rope:
             # q is rotated inside the attention kernel; k by the RoPE kernel
             # (it is also the returned cache).
