@@ -1,7 +1,8 @@
 """GPU tests of the layers on the HIP path (kernel_type 'flash' / 'triton'):
 the same layer weights give the reference semantics (oracle composition on
-the CPU) in fp32, and match the eager path in bf16 within the stated
-tolerance; caches hold the rotated keys."""
+the CPU) in fp32; against an fp64 eager reference of the same weights the HIP
+layer's error stays within twice the eager layer's own error in the same
+dtype; caches hold the rotated keys."""
 import pytest
 import torch
 
@@ -51,20 +52,34 @@ def test_hip_layer_fp32_matches_oracle(kind, feat, kernel_type):
 
 
 def test_hip_gqa_bf16_llama_block_matches_eager_and_cache():
+    """bf16 GQA block with RoPE (base 5e5), head_dim 128: the HIP layer's
+    error against an fp64 eager reference of the same weights is held to the
+    bf16 eager layer's own error (max within 2x + 1e-3 of the scale, mean
+    within 1.5x); measured 0.0557 vs 0.0564 (max) and 0.00251 vs 0.00253
+    (mean) of the scale."""
     torch.manual_seed(2)
     E, H, HKV = 1024, 8, 2  # head_dim 128
-    hip = tx.FastGroupedQueryAttention(E, H, HKV, causal=True, position_method="rope", rope_base=500000.0,
-                                       kernel_type="flash").cuda().to(torch.bfloat16)
-    eager = tx.FastGroupedQueryAttention(E, H, HKV, causal=True, position_method="rope", rope_base=500000.0,
-                                         kernel_type="pytorch").cuda().to(torch.bfloat16)
+
+    def make(kernel_type):
+        return tx.FastGroupedQueryAttention(E, H, HKV, causal=True, position_method="rope", rope_base=500000.0,
+                                            kernel_type=kernel_type)
+
+    hip = make("flash").cuda().to(torch.bfloat16)
+    eager = make("pytorch").cuda().to(torch.bfloat16)
     eager.load_state_dict(hip.state_dict())
+    r64 = make("pytorch").double()
+    r64.load_state_dict(hip.state_dict())
     x = torch.randn(2, 300, E, device="cuda").to(torch.bfloat16)
     o1, (k1, v1) = hip(x, use_cache=True)
     o2, (k2, v2) = eager(x, use_cache=True)
     assert torch.equal(k1, k2) and torch.equal(v1, v2)  # rotated keys bit-identical (RoPE kernel)
-    d = (o1.float() - o2.float()).abs()
-    scale = o2.float().abs().max().item()
-    assert d.max().item() <= 2e-2 * max(1.0, scale) and d.mean().item() <= 2e-3 * max(1.0, scale)
+    with torch.no_grad():
+        o64 = r64(x.double().cpu())[0]
+    scale = o64.abs().max().item()
+    dh = (o1.double().cpu() - o64).abs()
+    de = (o2.double().cpu() - o64).abs()
+    assert dh.max().item() <= 2 * de.max().item() + 1e-3 * scale, (dh.max().item(), de.max().item(), scale)
+    assert dh.mean().item() <= 1.5 * de.mean().item(), (dh.mean().item(), de.mean().item())
 
 
 def test_hip_layer_attention_mask_and_zero_attn():
@@ -114,51 +129,66 @@ def _layer_case(seed):
     return kind, D * H, H, dtype, kw, r.choice([1, 2]), r.randint(2, 200), r.random() < 0.5, r.random() < 0.5
 
 
+def _layer_run(m, x, train, decode, S, kind):
+    """Forward output, then the gradients of the input and of every parameter
+    (training) or three cached decode steps after a prefill (inference), all
+    as fp64 host tensors."""
+    xx = x.detach().clone().requires_grad_(train)
+    o = m(xx)
+    o = o[0] if isinstance(o, tuple) else o
+    grads = steps = None
+    if train:
+        o.to(torch.float64 if o.dtype == torch.float64 else torch.float32).square().mean().backward()
+        grads = [xx.grad.double().cpu()] + [p.grad.double().cpu() for p in m.parameters() if p.grad is not None]
+    elif decode and kind != "mhsa" and S > 4:
+        with torch.no_grad():
+            _, cache = m(x[:, :-3], use_cache=True)[:2]
+            outs = []
+            for t in range(3):
+                o1, cache = m(x[:, S - 3 + t:S - 2 + t], past_key_value=cache, use_cache=True)[:2]
+                outs.append(o1.double().cpu())
+            steps = torch.cat(outs, 1)
+    return o.detach().double().cpu(), grads, steps
+
+
 @pytest.mark.parametrize("seed", list(range(30)))
 def test_random_layer_flash_matches_pytorch_backend(seed):
     """Seeded random layer configurations (class, head_dim, heads, dtype,
-    causal, RoPE / ALiBi, sliding window, qk-norm type): the HIP path
-    (kernel_type='flash') against the layer's own eager backend
-    (kernel_type='pytorch', the restated reference path) with the same
-    weights.  Forward output, and either the gradients of the input and of
-    every parameter (training) or three cached decode steps after a prefill
-    (inference).  Bars: 1e-4 (fp32) / 3e-2 (bf16) of max(1, |out|) for
-    outputs; 2e-4 / 5e-2 of the largest gradient for gradients (the key
-    bias's own gradient is 0 up to rounding)."""
+    causal, RoPE / ALiBi, sliding window, qk-norm type) on the HIP path
+    (kernel_type='flash'), the layer's own eager backend in the same dtype
+    (kernel_type='pytorch', the restated reference path) and that eager
+    backend in fp64 on the host, all with the same weights.  Checked: the
+    forward output, and either the gradients of the input and of every
+    parameter (training) or three cached decode steps after a prefill
+    (inference).  Bar: the HIP error against fp64 is at most twice the eager
+    error in the same dtype plus 1e-3 (bf16) / 1e-6 (fp32) of the scale (the
+    output's largest magnitude; for a gradient, the largest parameter
+    gradient, since the key bias's own gradient is 0 up to rounding).
+    Measured across these seeds: worst HIP/eager ratio 1.5 (fp32 outputs),
+    1.13 (bf16 outputs) and 1.68 (bf16 gradients)."""
     kind, E, H, dtype, kw, B, S, train, decode = _layer_case(seed)
     print(f"seed {seed}: {kind} E{E} H{H} {dtype} B{B} S{S} train={train} {kw}", flush=True)
     torch.manual_seed(seed)
     hip = _make(kind, E, H, kernel_type="flash", **kw)[0].cuda().to(dtype)
-    ref = _make(kind, E, H, kernel_type="pytorch", **kw)[0].cuda().to(dtype)
-    ref.load_state_dict(hip.state_dict())
+    eager = _make(kind, E, H, kernel_type="pytorch", **kw)[0].cuda().to(dtype)
+    eager.load_state_dict(hip.state_dict())
+    r64 = _make(kind, E, H, kernel_type="pytorch", **kw)[0].double()
+    r64.load_state_dict(hip.state_dict())
     x = torch.randn(B, S, E, device="cuda", dtype=dtype)
-    tol, gtol = (1e-4, 2e-4) if dtype == torch.float32 else (3e-2, 5e-2)
-    res = []
-    for m in (hip, ref):
-        xx = x.detach().clone().requires_grad_(train)
-        o = m(xx)
-        o = o[0] if isinstance(o, tuple) else o
-        grads = None
-        if train:
-            o.float().square().mean().backward()
-            grads = [xx.grad.float()] + [p.grad.float() for p in m.parameters() if p.grad is not None]
-        res.append((o.detach().float(), grads))
-    (oh, gh), (orf, gr) = res
-    assert (oh - orf).abs().max().item() <= tol * max(1.0, orf.abs().max().item())
+    floor = 1e-6 if dtype == torch.float32 else 1e-3
+    (oh, gh, sh), (oe, ge, se) = (_layer_run(m, x, train, decode, S, kind) for m in (hip, eager))
+    o64, g64, s64 = _layer_run(r64, x.double().cpu(), train, decode, S, kind)
+
+    def check(h, e, ref, scale, what):
+        eh, ee = (h - ref).abs().max().item(), (e - ref).abs().max().item()
+        assert eh <= 2 * ee + floor * scale, (what, eh, ee, scale)
+
+    check(oh, oe, o64, o64.abs().max().item(), "output")
     if train:
-        assert len(gh) == len(gr)
-        assert (gh[0] - gr[0]).abs().max().item() <= gtol * gr[0].abs().max().item()
-        pscale = max(t.abs().max().item() for t in gr[1:])
-        for a, b in zip(gh[1:], gr[1:]):
-            assert (a - b).abs().max().item() <= gtol * pscale
-    elif decode and kind != "mhsa" and S > 4:
-        steps = []
-        with torch.no_grad():
-            for m in (hip, ref):
-                _, cache = m(x[:, :-3], use_cache=True)[:2]
-                outs = []
-                for t in range(3):
-                    o1, cache = m(x[:, S - 3 + t:S - 2 + t], past_key_value=cache, use_cache=True)[:2]
-                    outs.append(o1.float())
-                steps.append(torch.cat(outs, 1))
-        assert (steps[0] - steps[1]).abs().max().item() <= tol * max(1.0, steps[1].abs().max().item())
+        assert len(gh) == len(ge) == len(g64)
+        check(gh[0], ge[0], g64[0], g64[0].abs().max().item(), "input gradient")
+        pscale = max(t.abs().max().item() for t in g64[1:])
+        for n, (a, b, c) in enumerate(zip(gh[1:], ge[1:], g64[1:])):
+            check(a, b, c, pscale, f"parameter gradient {n}")
+    elif sh is not None:
+        check(sh, se, s64, s64.abs().max().item(), "decode steps")
