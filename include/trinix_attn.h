@@ -53,6 +53,9 @@
  *   trinix_dropout_state_advance <- no counterpart: the generator state torch keeps for
  *                                 the eager path's F.dropout under graph capture
  *                                 (trinix/layers/attention/base.py:395)
+ *   trinix_dropout_keep_map_bytes <- no counterpart: the size of the keep bits a dropout
+ *                                 forward leaves for its backward, where the eager path
+ *                                 keeps F.dropout's mask (base.py:395)
  */
 #ifndef TRINIX_ATTN_H
 #define TRINIX_ATTN_H
@@ -63,7 +66,7 @@
 extern "C" {
 #endif
 
-#define TRINIX_ATTN_ABI_VERSION 5
+#define TRINIX_ATTN_ABI_VERSION 6
 
 typedef enum trinix_status {
   TRINIX_OK = 0,
@@ -154,6 +157,18 @@ typedef struct trinix_attn_fwd_args {
    * (trinix_attn_bwd, then trinix_qk_norm_bwd) can use it.  NULL = not
    * written; requires q_norm_weight. */
   void* q_norm_out;
+  /* Dropout keep map (ABI version 6): with dropout_p > 0 the forward also
+   * writes its keep decisions here, one bit per (row, key), for a backward
+   * to read instead of regenerating them (trinix_attn_bwd_args).  bf16/fp16
+   * at head_dim 64 or 128 only (TRINIX_ERR_BAD_ARGUMENT otherwise), 16-byte
+   * aligned, trinix_dropout_keep_map_bytes bytes.  Layout, per (b, h) in
+   * order: 2*ceil(Sq/64) row blocks x 4*ceil(Sk/128) key blocks of 32 rows x
+   * 32 keys; a block is 32 uint32 words, word i % 32 for row i, whose bit
+   * 16h + 4q + e (h = 0, 1; q, e = 0..3) is set when key 8q + 4h + e of the
+   * block is kept.  Words of rows, keys or key tiles the forward does not
+   * visit (masked out, past Sq or Sk) are left as they were.
+   * NULL = not written. */
+  void* dropout_keep_map;
 } trinix_attn_fwd_args;
 
 /* Attention forward on `stream`. */
@@ -346,6 +361,11 @@ typedef struct trinix_attn_bwd_args {
   uint64_t dropout_seed;
   uint64_t dropout_offset;
   const uint64_t* dropout_state; /* the forward's, as in trinix_attn_fwd_args */
+  /* The keep map the forward wrote (ABI version 6), read in place of
+   * regenerating the keep mask: bf16/fp16 at head_dim 64 or 128 with
+   * dropout_p > 0 only (TRINIX_ERR_BAD_ARGUMENT otherwise).  NULL =
+   * regenerate from dropout_seed / dropout_offset / dropout_state. */
+  const void* dropout_keep_map;
 } trinix_attn_bwd_args;
 int trinix_attn_bwd(const trinix_attn_bwd_args* args, void* stream);
 
@@ -381,6 +401,14 @@ const char* trinix_status_string(int status);
  * forward and backward of that call read the same call_state.  Both
  * pointers are device memory, 8-byte aligned, two uint64 each. */
 int trinix_dropout_state_advance(uint64_t* generator, uint64_t* call_state, uint64_t increment, void* stream);
+
+/* Size in bytes of the dropout keep map of a (batch, nheads_q, seqlen_q,
+ * seqlen_k) attention: 128 * batch * nheads_q * 2*ceil(seqlen_q/64) *
+ * 4*ceil(seqlen_k/128).  No counterpart in the reference, whose eager path
+ * keeps F.dropout's mask of the attention weights for its backward
+ * (trinix/layers/attention/base.py:395) at one element per (row, key). */
+int trinix_dropout_keep_map_bytes(int64_t batch, int64_t nheads_q, int64_t seqlen_q, int64_t seqlen_k,
+                                  int64_t* bytes);
 
 /* TRINIX_ATTN_ABI_VERSION of the built library. */
 int trinix_abi_version(void);

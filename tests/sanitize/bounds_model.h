@@ -18,6 +18,8 @@
 //     allowed (row, key) pairs;
 //   * split-KV chunks tile the visible keys and partial results stay inside
 //     the workspace.
+//   * with a dropout keep map, the words the forward writes and the 256-byte
+//     copies the backward makes of it lie inside the map (index_map.h).
 // The per-lane load formulas that are not in index_map.h (a row's q, K/V,
 // mask and output addresses: base + b*sb + h*sh + row*ss) are restated here
 // from the kernels, each next to the kernel line it follows.
@@ -225,6 +227,22 @@ inline void model_fwd16(Report& R, const trinix_attn_fwd_args& a, const FwdPlan&
       if (a.mask && a.mask_blockmap && live)
         R.expect(iw0 / 32 < bmap_rows, "fwd block map", "row block %lld of %lld", iw0 / 32, bmap_rows);
       (void)bmap_cols;
+      if (a.dropout_keep_map && a.dropout_p > 0.f && live) {
+        // half g of word r of block (iw0/32, tile*BN/32 + nb) (attn_kernel16.h softmax, DROP == 2)
+        const int64_t nbi = keep_map_nbi(Sq), nbj = keep_map_nbj(Sk), words = (int64_t)B * Hq * nbi * nbj * 32;
+        for (int t : {tr.t_lo, tr.t_hi - 1}) {
+          if (t < tr.t_lo || t >= tr.t_hi || (t - tr.t_lo) % rb.ks != kp) continue;
+          for (int nb = 0; nb < BN / 32; ++nb) {
+            const int64_t bi = iw0 >> 5, bj = (((int64_t)t * BN) >> 5) + nb;
+            R.expect(bi < nbi && bj < nbj, "fwd keep map", "block (%lld, %lld) of (%lld, %lld)", bi, bj, nbi, nbj);
+            for (int r : {0, 31})
+              for (int g : {0, 1}) {
+                const int64_t half = 2 * (keep_map_block((int64_t)it.b * Hq + hq, bi, bj, nbi, nbj) + r) + g;
+                R.expect(half >= 0 && half < 2 * words, "fwd keep map", "half-word %lld of %lld", half, 2 * words);
+              }
+          }
+        }
+      }
     }
   }
   if (all) {
@@ -286,6 +304,19 @@ inline void model_bwd16(Report& R, const trinix_attn_bwd_args& a, const BwdPlan&
         const int64_t row = i0 + imin(lane, Sq - 1 - i0);
         R.expect(row >= 0 && row < Sq, "dkdv lse", "row %lld", row);
       }
+      if (a.dropout_keep_map && a.dropout_p > 0.f) {
+        // load_item: 4 copies of 64 words, block (qt*2 + c/2, kblk*4) + (c%2)*64 + lane
+        const int64_t nbi = keep_map_nbi(Sq), nbj = keep_map_nbj(Sk), words = (int64_t)B * Hq * nbi * nbj * 32;
+        for (int gh : {0, G - 1})
+          for (int c = 0; c < 4; ++c) {
+            const int64_t bi = (int64_t)qt * 2 + (c >> 1), bj = (int64_t)it.kblk * 4;
+            R.expect(bi < nbi && bj + 3 < nbj, "dkdv keep map", "blocks (%lld, %lld..+3) of (%lld, %lld)", bi, bj, nbi,
+                     nbj);
+            const int64_t base = keep_map_block((int64_t)it.b * Hq + it.hkv * G + gh, bi, bj, nbi, nbj) + (c & 1) * 64;
+            R.expect(base >= 0 && base + 63 < words, "dkdv keep map", "words [%lld, %lld] of %lld", base, base + 63,
+                     words);
+          }
+      }
       if (a.mask) {
         for (int st = 0; st < BQ / 32; ++st) {  // attn_bwd16.h stage A, 64-bit sub-tile row + 32-bit offsets
           const int ia = i0 + st * 32;
@@ -345,6 +376,26 @@ inline void model_bwd16(Report& R, const trinix_attn_bwd_args& a, const BwdPlan&
       if (t < t_lo || t >= t_hi) continue;
       check_tile_copy(R, "dq K tile", (int64_t)t * BN, BN, D, NW, 2, Sk, a.k_stride[1], true);
       check_tile_copy(R, "dq V tile", (int64_t)t * BN, BN, D, NW, 2, Sk, a.v_stride[1], true);
+    }
+    if (a.dropout_keep_map && a.dropout_p > 0.f) {
+      // load_keep: the wavefront's NB/2 copies of 64 words, block (iw0/32, t*NB) + c*64 + lane
+      const int NB = BN / 32;
+      const int64_t nbi = keep_map_nbi(Sq), nbj = keep_map_nbj(Sk), words = (int64_t)B * Hq * nbi * nbj * 32;
+      for (int t : {t_lo, t_hi - 1}) {
+        if (t < t_lo || t >= t_hi) continue;
+        for (int w = 0; w < NW; ++w) {
+          const int iw0 = it.m0 + w * 32;
+          if (iw0 >= Sq) continue;
+          const int64_t bi = iw0 >> 5, bj = (int64_t)t * NB;
+          R.expect(bi < nbi && bj + NB - 1 < nbj, "dq keep map", "blocks (%lld, %lld..) of (%lld, %lld)", bi, bj, nbi,
+                   nbj);
+          for (int c = 0; c < NB / 2; ++c) {
+            const int64_t base = keep_map_block((int64_t)it.b * Hq + hq, bi, bj, nbi, nbj) + c * 64;
+            R.expect(base >= 0 && base + 63 < words, "dq keep map", "words [%lld, %lld] of %lld", base, base + 63,
+                     words);
+          }
+        }
+      }
     }
     for (int w = 0; w < NW; ++w)
       for (int r = 0; r < 32; ++r) {

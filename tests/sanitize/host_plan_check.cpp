@@ -309,6 +309,7 @@ int main() {
       b.nheads_kv = f.nheads_kv, b.head_dim = f.head_dim, b.dtype = f.dtype, b.causal = f.causal;
       b.has_window = f.has_window, b.window_left = f.window_left, b.window_right = f.window_right;
       b.mask = f.mask, b.mask_dtype = f.mask_dtype, b.mask_blockmap = f.mask_blockmap, b.dropout_p = f.dropout_p;
+      b.dropout_keep_map = f.dropout_keep_map;
       for (int i = 0; i < 4; ++i) {
         b.q_stride[i] = b.dout_stride[i] = b.out_stride[i] = b.dq_stride[i] = f.q_stride[i];
         b.k_stride[i] = b.dk_stride[i] = f.k_stride[i];
@@ -349,9 +350,14 @@ int main() {
             if (c >= 2) a.has_window = 1, a.window_left = c == 4 ? -3 : 40, a.window_right = c == 5 ? (1ll << 62) : 7;
             if (c == 3) a.mask = (void*)4096, a.mask_dtype = TRINIX_BF16, a.mask_blockmap = (const uint8_t*)4096,
                         a.mask_stride[2] = Sk, a.mask_stride[3] = 1;
-            if (c == 5) a.dropout_p = 0.25f;
+            if (c == 5) a.dropout_p = 0.25f, a.dropout_keep_map = D <= 128 ? (void*)4096 : nullptr;
             add(a);
           }
+    a = shape(4, 1024, 1024, 12, 12, 64, TRINIX_BF16), a.causal = 1;                     // C2, C3 with dropout
+    a.dropout_p = 0.1f, a.dropout_keep_map = (void*)4096, add(a);
+    a = shape(1, 8192, 8192, 32, 8, 128, TRINIX_BF16), a.causal = 1;
+    a.dropout_p = 0.1f, a.dropout_keep_map = (void*)4096, add(a);
+    a = shape(3, 300, 77, 6, 2, 64, TRINIX_F16), a.dropout_p = 0.3f, a.dropout_keep_map = (void*)4096, add(a);
     a = shape(1, 40000, 40000, 2, 1, 64, TRINIX_BF16), a.causal = 1, a.has_window = 1;  // long, two-sided window
     a.window_left = 8192, a.window_right = 300, add(a);
     a = shape(3, 9, 70000, 32, 8, 128, TRINIX_BF16), a.causal = 1, add(a);              // decode shapes
@@ -390,6 +396,10 @@ int main() {
         a.mask_blockmap = next_u64() % 2 ? (const uint8_t*)4096 : nullptr;
         a.mask_stride[0] = rand_size(), a.mask_stride[1] = rand_size();
         a.mask_stride[2] = rand_size(), a.mask_stride[3] = next_u64() % 2 ? 1 : rand_size();
+      }
+      if (next_u64() % 4 == 0) {
+        a.dropout_p = 0.1f;
+        if (a.head_dim <= 128) a.dropout_keep_map = (void*)4096;
       }
       if (validate_fwd_args(&a) != TRINIX_OK) continue;
       model_one(a, 4096);

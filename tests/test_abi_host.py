@@ -108,10 +108,60 @@ def _args(**kw):
     (dict(mask=4096, mask_dtype=nat.TRINIX_F32, mask_stride=nat.int64x4((0, 0, -64, 1))), nat.TRINIX_ERR_BAD_STRIDE),
     (dict(mask=4096, mask_dtype=nat.TRINIX_F32, mask_stride=nat.int64x4((0, 0, 1 << 27, 1))),
      nat.TRINIX_ERR_BAD_STRIDE),
+    # a dropout keep map: with dropout, 16-byte aligned, bf16/fp16 at head_dim 64/128
+    (dict(dropout_keep_map=4096), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(dropout_p=0.1, dropout_keep_map=4104), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(dropout_p=0.1, dropout_keep_map=4096, dtype=nat.TRINIX_F32), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(dropout_p=0.1, dropout_keep_map=4096, head_dim=256,
+          **{n: nat.int64x4((8 * 64 * 256, 8 * 256, 256, 1)) for n in ("q_stride", "k_stride", "v_stride",
+                                                                       "out_stride")}),
+     nat.TRINIX_ERR_BAD_ARGUMENT),
 ])
 def test_validation_rejects_before_launch(lib, kw, code):
     a = _args(**kw)
     assert lib.trinix_attn_fwd(ctypes.byref(a), None) == code
+
+
+def _bwd_args(**kw):
+    a = nat.AttnBwdArgs()
+    a.q = a.k = a.v = a.out = a.dout = a.lse = a.delta = a.dq = a.dk = a.dv = 4096
+    for name in ("q", "k", "v", "out", "dout", "dq", "dk", "dv"):
+        setattr(a, name + "_stride", nat.int64x4((8 * 64 * 128, 8 * 128, 128, 1)))
+    a.batch, a.seqlen_q, a.seqlen_k, a.nheads_q, a.nheads_kv, a.head_dim = 1, 64, 64, 8, 8, 128
+    a.dtype = nat.TRINIX_BF16
+    a.softmax_scale = 0.1
+    for k_, v_ in kw.items():
+        setattr(a, k_, v_)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(dropout_p=1.0), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(lse=None), nat.TRINIX_ERR_NULL_POINTER),
+    (dict(dropout_keep_map=4096), nat.TRINIX_ERR_BAD_ARGUMENT),  # a keep map without dropout
+    (dict(dropout_p=0.1, dropout_keep_map=4100), nat.TRINIX_ERR_BAD_ARGUMENT),
+    (dict(dropout_p=0.1, dropout_keep_map=4096, dtype=nat.TRINIX_F32), nat.TRINIX_ERR_BAD_ARGUMENT),
+])
+def test_backward_validation_rejects_before_launch(lib, kw, code):
+    a = _bwd_args(**kw)
+    assert lib.trinix_attn_bwd(ctypes.byref(a), None) == code
+
+
+def test_dropout_keep_map_bytes(lib):
+    """128 bytes per 32x32 block, 2*ceil(Sq/64) x 4*ceil(Sk/128) blocks per
+    (batch, head): every 64-row item and 128-key group of the backward's
+    tile copies lies inside the map."""
+    n = ctypes.c_int64(0)
+    for B, H, Sq, Sk in [(1, 1, 1, 1), (1, 32, 8192, 8192), (2, 3, 65, 129), (4, 12, 1024, 1024), (1, 1, 64, 128)]:
+        assert lib.trinix_dropout_keep_map_bytes(B, H, Sq, Sk, ctypes.byref(n)) == 0
+        nbi, nbj = 2 * -(-Sq // 64), 4 * -(-Sk // 128)
+        assert n.value == 128 * B * H * nbi * nbj
+        assert nbi * 32 >= Sq and nbj * 32 >= Sk and nbi % 2 == 0 and nbj % 4 == 0
+    lib.trinix_dropout_keep_map_bytes(1, 32, 8192, 8192, ctypes.byref(n))
+    assert n.value == 268435456  # 1/8 byte per (row, key) at full tiles
+    assert lib.trinix_dropout_keep_map_bytes(0, 1, 1, 1, ctypes.byref(n)) == nat.TRINIX_ERR_BAD_SHAPE
+    assert lib.trinix_dropout_keep_map_bytes(1, 1, 1 << 30, 1, ctypes.byref(n)) == nat.TRINIX_ERR_BAD_SHAPE
+    assert lib.trinix_dropout_keep_map_bytes(1, 1, 1, 1, None) == nat.TRINIX_ERR_NULL_POINTER
 
 
 def test_status_to_exception_types(lib):

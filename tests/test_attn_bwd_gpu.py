@@ -333,13 +333,17 @@ DROP_CASES = [
 ]
 
 
+@pytest.mark.parametrize("keep_map", ["1", "0"])
 @pytest.mark.parametrize("case", range(len(DROP_CASES)))
-def test_dropout_backward_matches_eager_with_philox_keep(case):
+def test_dropout_backward_matches_eager_with_philox_keep(case, keep_map, monkeypatch):
     """Forward and gradients with dropout against eager autograd of the
     oracle using the kernel's keep mask (the Philox stream the oracle
-    restates), so the backward must regenerate exactly the forward's mask."""
+    restates), so the backward must use exactly the forward's mask: read
+    from the forward's keep map (bf16/fp16 at head_dim 64/128), or
+    regenerated (TRINIX_DROPOUT_KEEP_MAP=0, and the generic kernels)."""
+    monkeypatch.setenv("TRINIX_DROPOUT_KEEP_MAP", keep_map)
     B, Sq, Sk, H, Hkv, D, dtype, p, kw = DROP_CASES[case]
-    print(f"dropout backward case {DROP_CASES[case][:8]}", flush=True)
+    print(f"dropout backward case {DROP_CASES[case][:8]} keep map {keep_map}", flush=True)
     q, k, v, do = _inputs(B, Sq, Sk, H, Hkv, D, seed=500 + case)
     torch.manual_seed(4321)
     seed = int(torch.randint(0, 2 ** 62, (1,)).item())

@@ -44,13 +44,16 @@ def test_host_plan_under_asan_ubsan(tmp_path):
 
 # Mistakes planted in a copy of index_map.h: each must make the bounds model
 # report failures (an off-by-one tile count, a lane offset one unit off, a
-# row block map that skips a block, a query range that drops a tile).
+# row block map that skips a block, a query range that drops a tile, a
+# decode chunk past the keys, an unpadded dropout keep map).
 PLANTED = [
     ("tr.t_hi = hi > lo ? (int)((hi + BN - 1) / BN) : tr.t_lo;", "tr.t_hi = hi > lo ? (int)(hi / BN) : tr.t_lo;"),
     ("return row * (uint32_t)ss * 2u + unit * 16u;", "return row * (uint32_t)ss * 2u + unit * 16u + 16u;"),
     ("const int mblk = causal ? (num_mblk - 1 - mi) : mi;", "const int mblk = causal ? (num_mblk - 1 - mi) : (mi ? mi - 1 : 0);"),
     ("qt_hi = i_hi > i_lo ? (i_hi + BQ - 1) / BQ : qt_lo;", "qt_hi = i_hi > i_lo ? (i_hi + BQ - 1) / BQ - (kb0 > 0) : qt_lo;"),
     ("c1 = imin(khi, c0 + chunk);", "c1 = imin(khi + 64, c0 + chunk);"),
+    # a keep map without the padding to whole 128-key groups
+    ("return 4 * ((Sk + 127) / 128);", "return (Sk + 31) / 32;"),
 ]
 
 

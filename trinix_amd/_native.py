@@ -40,7 +40,7 @@ TRINIX_NORM_LAYER = 1
 BLOCKMAP_ROWS = 32
 BLOCKMAP_COLS = 64
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 Int64x4 = c_int64 * 4
 Int64x2 = c_int64 * 2
@@ -88,6 +88,7 @@ class AttnFwdArgs(ctypes.Structure):
         ("q_norm_eps", c_float),
         ("dropout_state", c_void_p),
         ("q_norm_out", c_void_p),
+        ("dropout_keep_map", c_void_p),
     ]
 
 
@@ -136,6 +137,7 @@ class AttnBwdArgs(ctypes.Structure):
         ("dropout_seed", c_uint64),
         ("dropout_offset", c_uint64),
         ("dropout_state", c_void_p),
+        ("dropout_keep_map", c_void_p),
     ]
 
 
@@ -186,6 +188,7 @@ SIGNATURES = {
     "trinix_alibi_bias": (c_int32, [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p]),
     "trinix_attn_tile_config": (c_int32, [c_int64, c_int32, POINTER(TileCfg)]),
     "trinix_dropout_state_advance": (c_int32, [c_void_p, c_void_p, c_uint64, c_void_p]),
+    "trinix_dropout_keep_map_bytes": (c_int32, [c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "trinix_attn_is_available": (c_int32, []),
     "trinix_status_string": (c_char_p, [c_int32]),
     "trinix_abi_version": (c_int32, []),

@@ -121,6 +121,9 @@ extern "C" int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* stream) {
   p.off_lo = (uint32_t)a->dropout_offset;
   p.off_hi = (uint32_t)(a->dropout_offset >> 32);
   p.drop_state = a->dropout_state;
+  p.keep_map = (const uint32_t*)a->dropout_keep_map;
+  p.km_nbi = keep_map_nbi(a->seqlen_q);
+  p.km_nbj = keep_map_nbj(a->seqlen_k);
   const int feat = (a->alibi_slopes ? kFeatAlibi : 0) | (a->mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0);
 
   hipStream_t st = (hipStream_t)stream;

@@ -66,6 +66,8 @@ struct BwdParams {
   float drop_scale;      // 1 / (1 - p)
   uint32_t seed_lo, seed_hi, off_lo, off_hi;
   const uint64_t* drop_state;  // {seed, offset} in device memory, read in place of the four above; or null
+  const uint32_t* keep_map;    // the forward's keep bits (index_map.h), read in place of Philox; or null
+  int64_t km_nbi, km_nbj;      // its row / key blocks per (batch, q-head)
 };
 
 // Allowed (i, j): j - i in [dlo, dhi] (causal: j <= i; window: -wl <= j-i <= wr).
@@ -174,8 +176,54 @@ __device__ inline uint32_t keep_bits_of_key(const DropKey& dkey, int bh, int j, 
   // rows v = q and q + 8 come from lane q of the group
   return gather_keep_bits(own, e8, std::make_integer_sequence<int, 8>{});
 }
-// All ones when bit v of keep bits m is set, else 0 (one v_bfe_i32).
-__device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int)(m << (31 - v)) >> 31); }
+
+// x of lane l ^ S, within each 32-lane half (S = 1, 2: quad permutes; 4, 8:
+// two row shifts into alternate banks; 16: v_permlane16_swap, which trades
+// the odd 16-lane rows of its first operand with the even rows of its
+// second, the partner's value then in the first result on odd rows).
+template <int S>
+__device__ inline uint32_t xor_lane(uint32_t x, int lane) {
+  if constexpr (S == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0xb1, 0xf, 0xf, false);  // [1,0,3,2]
+  if constexpr (S == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4e, 0xf, 0xf, false);  // [2,3,0,1]
+  if constexpr (S == 4 || S == 8) {
+    // row_shl:S into the banks whose lane bit S is clear, row_shr:S into the others
+    const int t = __builtin_amdgcn_update_dpp((int)x, (int)x, 0x100 | S, 0xf, S == 4 ? 0x5 : 0x3, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)x, 0x110 | S, 0xf, S == 4 ? 0xa : 0xc, false);
+  }
+  if constexpr (S == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  }
+  return x;
+}
+// One stage of a bit transpose of a 32x32 block held a word per lane: lane
+// index bit S trades places with word bit T.  Of lanes l and l ^ S, the one
+// with lane bit S clear keeps its bits whose bit-T index is clear and takes
+// the partner's such bits, moved up by T, into the others; the other lane
+// keeps its bits with bit-T index set and takes the partner's moved down.
+template <int S, int T>
+__device__ inline uint32_t transpose_stage(uint32_t a, int lane) {
+  constexpr uint32_t M = T == 16 ? 0x0000ffffu : T == 8 ? 0x00ff00ffu : T == 4 ? 0x0f0f0f0fu : T == 2 ? 0x33333333u : 0x55555555u;
+  const uint32_t t = xor_lane<S>(a, lane);
+  const bool up = (lane & S) != 0;
+  const uint32_t y = __builtin_amdgcn_alignbit(t, t, up ? T : 32 - T);  // rotate right
+  const uint32_t m = up ? ~M : M;
+  return (a & m) | (y & ~m);
+}
+// Keep words of a 32x32 block, one row per lane (lane l: row l % 32, both
+// lane halves alike), the row's keys in the keep map's order (bit
+// 16h + 4q + e: key 8q + 4h + e).  Returns, for the lane's key l % 32, the
+// rows in the same order: bit 16h + 4q + e for row 8q + 4h + e.  The five
+// stages trade lane bits 4, 3, 2, 1, 0 with word bits 3, 2, 4, 1, 0, which
+// turns the map's key order into the key index and the row index into that
+// order.
+__device__ inline uint32_t transpose_keep_block(uint32_t a, int lane) {
+  a = transpose_stage<16, 8>(a, lane);
+  a = transpose_stage<8, 4>(a, lane);
+  a = transpose_stage<4, 16>(a, lane);
+  a = transpose_stage<2, 2>(a, lane);
+  return transpose_stage<1, 1>(a, lane);
+}
 
 // ---------------------------------------------------------------------------
 // dK, dV: a two-stage pipeline over two wavefronts per 32-key group.  Lane l
@@ -204,7 +252,7 @@ __device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int
 // Pd = keep P/(1-p) and of dZ = P (keep dP/(1-p) - delta) = dZ'/(1-p) is
 // applied once per output element in the epilogue.
 // ---------------------------------------------------------------------------
-template <class E, int D, bool ALIBI, bool MASK, bool DROP>
+template <class E, int D, bool ALIBI, bool MASK, int DROP>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   DropKey dkey{};
   if constexpr (DROP) dkey = drop_key(p);
@@ -220,6 +268,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   __shared__ __attribute__((aligned(256))) float lds_l[NSL * BQ];
   __shared__ __attribute__((aligned(256))) float lds_d[NSL * BQ];
   __shared__ __attribute__((aligned(256))) uint32_t lds_m[DROP ? 2 * NG * NST * 64 : 1];  // keep bits
+  // the item's rows of the keep map (slot, sub-tile st, key group kg, row): DROP == 2
+  __shared__ __attribute__((aligned(256))) uint32_t lds_kw[DROP == 2 ? NSL * NST * NG * 32 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -278,6 +328,18 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
     const int64_t vo = ((int64_t)b * p.Hq + hq) * p.Sq;
     if (wave == 0) load_vec(p.lse + vo, lds_l + SL * BQ, i0);
     if (wave == 1) load_vec(p.delta + vo, lds_d + SL * BQ, i0);
+    if constexpr (DROP == 2) {
+      // keep words of the item's two 32-row blocks and the workgroup's four
+      // 32-key blocks: per row block 512 consecutive bytes, two copies of
+      // 256 (waves 2..5, one each)
+      if (wave >= 2 && wave < 6) {
+        const int c = wave - 2, st = c >> 1;
+        const uint64_t gb = uniform_ptr(p.keep_map + keep_map_block((int64_t)b * p.Hq + hq, it.qt * 2 + st, kblk * 4,
+                                                                    p.km_nbi, p.km_nbj) + (c & 1) * 64);
+        dma_4b_s((uint32_t)lane * 4u, gb,
+                 __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)(lds_kw + SL * NST * NG * 32 + c * 64)));
+      }
+    }
   };
   // Does sub-tile st of the item hold allowed pairs for this wavefront's keys
   // (band, bounds, block map)?  Both stages take the same decision, so stage
@@ -460,8 +522,14 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
           *p_slot(PS, st, kk) = pb[kk];
         }
         if constexpr (DROP) {
-          // dV takes the dropped, rescaled P of the forward's PV product
-          const uint32_t km = keep_bits_of_key(dkey, b * p.Hq + hq, j, i0 + st * 32 + g * 4);
+          // dV takes the dropped P of the forward's PV product.  Keep bits of
+          // the lane's key, row r(v) at bit v: from the forward's keep map
+          // (the block's row words, transposed), or regenerated
+          uint32_t km;
+          if constexpr (DROP == 2)
+            km = transpose_keep_block(lds_kw[(SL * NST + st) * NG * 32 + kg * 32 + (lane & 31)], lane) >> (16 * g);
+          else
+            km = keep_bits_of_key(dkey, b * p.Hq + hq, j, i0 + st * 32 + g * 4);
           *m_slot(PS, st) = km;
 #pragma unroll
           for (int v = 0; v < 16; ++v) x[v] = __uint_as_float(__float_as_uint(x[v]) & keep_word(km, v));
@@ -585,7 +653,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 // drawn as the forward draws them: the two lanes of a row share the calls
 // of 8-key group pairs (philox_pair_words).
 // ---------------------------------------------------------------------------
-template <class E, int D, bool ALIBI, bool MASK, bool DROP, int NW, int BN>
+template <class E, int D, bool ALIBI, bool MASK, int DROP, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
   DropKey dkey{};
   if constexpr (DROP) dkey = drop_key(p);
@@ -597,6 +665,8 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
   __shared__ __attribute__((aligned(1024))) uint16_t lds_k1[BN * D];
   __shared__ __attribute__((aligned(1024))) uint16_t lds_v0[BN * D];
   __shared__ __attribute__((aligned(1024))) uint16_t lds_v1[BN * D];
+  // keep words of the tile's rows (slot, wavefront, 32-key block, row): DROP == 2
+  __shared__ __attribute__((aligned(256))) uint32_t lds_kq[DROP == 2 ? 2 * NW * NB * 32 : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -667,7 +737,24 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
   // `edge` is a runtime flag and only the masking of the scores branches on
   // it (two instantiated copies of the dQ MFMAs cost 64 accumulator moves at
   // every join).
-  auto tile_body = [&](bool edge, const uint16_t* kt, const uint16_t* vt, int t) __attribute__((always_inline)) {
+  // Keep words of this wavefront's 32 rows for tile t: the tile's NB blocks
+  // of 128 bytes are consecutive in the map, 256 bytes per copy.
+  auto load_keep = [&](uint32_t* slot_words, int t) __attribute__((always_inline)) {
+    if constexpr (DROP == 2) {
+      if (iw0 < p.Sq) {
+#pragma unroll
+        for (int c = 0; c < NB / 2; ++c) {
+          const uint64_t gb = uniform_ptr(p.keep_map + keep_map_block((int64_t)b * p.Hq + hq, iw0 >> 5, (int64_t)t * NB,
+                                                                      p.km_nbi, p.km_nbj) + c * 64);
+          dma_4b_s((uint32_t)lane * 4u, gb,
+                   __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_t*)(slot_words + wave * NB * 32 + c * 64)));
+        }
+      }
+    }
+  };
+
+  auto tile_body = [&](bool edge, const uint16_t* kt, const uint16_t* vt, const uint32_t* kq, int t)
+                       __attribute__((always_inline)) {
     const int n0 = t * BN;
     int mcode = 1;
     if constexpr (MASK) {
@@ -738,7 +825,17 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
       u32x4_t zb[2];
       {
         float z[16];
-        if constexpr (DROP && ALIBI && MASK && D == 128) {
+        if constexpr (DROP == 2) {
+          // keep bits of the row's 16 elements of the block (bit v: element v,
+          // key (v/4)*8 + 4g + v%4): half g of row i's word of the forward's
+          // keep map
+          const uint32_t km = kq[wave * NB * 32 + nb * 32 + r] >> (16 * g);
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const float dpk = __uint_as_float(__float_as_uint(dp[v]) & keep_word(km, v));
+            z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dpk - dlt);
+          }
+        } else if constexpr (DROP && ALIBI && MASK && D == 128) {
           // every register in use: each lane makes the call of its own 8-key
           // group and keeps its 4 fields (4g..4g+3), one group at a time
 #pragma unroll
@@ -801,6 +898,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
   if (t_lo < t_hi) {
     load_rows(kbase, p.k_ss, lds_k0, t_lo);
     load_rows(vbase, p.v_ss, lds_v0, t_lo);
+    load_keep(lds_kq, t_lo);
   }
   const bool wave_live = iw0 < p.Sq;
   auto step = [&](auto slot_c, int t) __attribute__((always_inline)) {
@@ -810,6 +908,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
     if (t + 1 < t_hi) {
       load_rows(kbase, p.k_ss, SL ? lds_k0 : lds_k1, t + 1);
       load_rows(vbase, p.v_ss, SL ? lds_v0 : lds_v1, t + 1);
+      load_keep(lds_kq + (1 - SL) * NW * NB * 32, t + 1);
     }
     const uint16_t* kt = SL ? lds_k1 : lds_k0;
     const uint16_t* vt = SL ? lds_v1 : lds_v0;
@@ -818,7 +917,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
     const int nl = min(n0 + BN, p.Sk) - 1;
     if (!wave_live || n0 - iwl > band.dhi || nl - iw0 < band.dlo) return;  // no allowed pair
     const bool full = iw0 + 31 < p.Sq && n0 + BN <= p.Sk && nl - iw0 <= band.dhi && n0 - iwl >= band.dlo;
-    tile_body(!full, kt, vt, t);
+    tile_body(!full, kt, vt, lds_kq + SL * NW * NB * 32, t);
   };
   int t = t_lo;
   for (; t + 1 < t_hi; t += 2) {
@@ -845,20 +944,33 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 
 // Launch of both gradient kernels for one (dtype, D); feat = kFeatAlibi |
 // kFeatMask | kFeatDropout.
-template <class E, int D>
-hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
+// Launch of both gradient kernels of one feature set; DROP as in the
+// kernels (0 none, 1 regenerated keep mask, 2 the forward's keep map).
+template <class E, int D, bool A, bool M, int DROP>
+hipError_t launch_bwd_pair(const BwdParams& p, hipStream_t st) {
   const dim3 g_kv((unsigned)(p.B * p.Hkv * p.num_kblk)), g_q((unsigned)(p.B * p.Hq * p.num_mblk)), blk(256),
       blk_kv(512);
+  const hipError_t e = launch_kernel(&attn_bwd_dkdv<E, D, A, M, DROP>, g_kv, blk_kv, 0, st, p);
+  if (e != hipSuccess) return e;
+  if constexpr (D == 128 && !M)
+    if (p.dq_wide) return launch_kernel(&attn_bwd_dq<E, D, A, M, DROP, 8, 128>, g_q, blk_kv, 0, st, p);
+  return launch_kernel(&attn_bwd_dq<E, D, A, M, DROP, 4, 64>, g_q, blk, 0, st, p);
+}
+
+// Launch of both gradient kernels for one (dtype, D); feat = kFeatAlibi |
+// kFeatMask | kFeatDropout (with p.keep_map: the map-reading variants).
+template <class E, int D>
+hipError_t launch_bwd(const BwdParams& p, int feat, hipStream_t st) {
   switch (feat & 7) {
 #define TRINIX_BWD_CASE(F)                                                                                \
   case F:                                                                                                 \
   {                                                                                                       \
     constexpr bool A = (F & kFeatAlibi) != 0, M = (F & kFeatMask) != 0, DR = (F & kFeatDropout) != 0;     \
-    const hipError_t e = launch_kernel(&attn_bwd_dkdv<E, D, A, M, DR>, g_kv, blk_kv, 0, st, p);           \
-    if (e != hipSuccess) return e;                                                                        \
-    if constexpr (D == 128 && !M)                                                                         \
-      if (p.dq_wide) return launch_kernel(&attn_bwd_dq<E, D, A, M, DR, 8, 128>, g_q, blk_kv, 0, st, p);    \
-    return launch_kernel(&attn_bwd_dq<E, D, A, M, DR, 4, 64>, g_q, blk, 0, st, p);                        \
+    if constexpr (DR) {                                                                                   \
+      if (p.keep_map) return launch_bwd_pair<E, D, A, M, 2>(p, st);                                       \
+      return launch_bwd_pair<E, D, A, M, 1>(p, st);                                                       \
+    }                                                                                                     \
+    return launch_bwd_pair<E, D, A, M, 0>(p, st);                                                         \
   }
     TRINIX_BWD_CASE(0)
     TRINIX_BWD_CASE(1)

@@ -390,6 +390,9 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
   p.qn_w = (const uint16_t*)a->q_norm_weight;
   p.qn_eps = a->q_norm_eps;
   p.qn_out = (uint16_t*)a->q_norm_out;
+  p.keep_map = (uint32_t*)a->dropout_keep_map;
+  p.km_nbi = keep_map_nbi(a->seqlen_q);
+  p.km_nbj = keep_map_nbj(a->seqlen_k);
 
   hipStream_t st = (hipStream_t)stream;
   hipError_t err;
@@ -400,7 +403,7 @@ int trinix_attn_fwd(const trinix_attn_fwd_args* a, void* stream) {
     else err = launch_kernel(&attn_fwd_f32<256, kWavesF32>, grid, block, 0, st, p);
   } else {
     const int feat = (p.alibi ? kFeatAlibi : 0) | (p.mask ? kFeatMask : 0) | (p.use_dropout ? kFeatDropout : 0) |
-                     (p.qn_w ? kFeatQNorm : 0);
+                     (p.qn_w ? kFeatQNorm : 0) | (p.use_dropout && p.keep_map ? kFeatKeepMap : 0);
     const bool bf = a->dtype == TRINIX_BF16;
     if (a->head_dim == 64)
       err = bf ? launch_attn16_bf16_d64(p, cfg, feat, st) : launch_attn16_f16_d64(p, cfg, feat, st);

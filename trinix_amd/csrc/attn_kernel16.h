@@ -42,10 +42,13 @@
 
 namespace trinix {
 
-template <class E, int D, int BN, int NW, int OCC, int KS, bool ALIBI, bool MASK, bool DROP, bool QN>
+// DROP: 0 no dropout, 1 dropout, 2 dropout that also writes the keep map
+// (p.keep_map, index_map.h) for the backward.
+template <class E, int D, int BN, int NW, int OCC, int KS, bool ALIBI, bool MASK, int DROP, bool QN>
 // The head_dim 64 mask kernels are held to three wavefronts per SIMD (168
-// VGPRs); the other shapes to OCC.
-__global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd_mfma16(const FwdParams p) {
+// VGPRs), except the one writing a keep map (it does not fit); the other
+// shapes to OCC.
+__global__ __launch_bounds__(NW * 64, (MASK && D == 64 && DROP != 2) ? 3 : OCC) void attn_fwd_mfma16(const FwdParams p) {
   // KS = 2 splits each 32-row group's keys between two wavefronts: wavefront
   // 2r + kp owns rows 32r..32r+31 and the tiles t_lo + KS*s + kp; the halves
   // merge through LDS at the end.  It halves the longest dependency chain of
@@ -455,6 +458,25 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
     for (int m = 0; m < VPF; ++m) vpre[m] = vread(vt, m);
   };
 
+  // Keep map (DROP == 2): a tile's keep bits (half g of row i's word of each
+  // 32-key block, index_map.h) are stored at the start of the wavefront's
+  // next tile, after its loads are issued, or after the last tile.  Stored at
+  // once, the step's s_waitcnt at the next tile would wait for the stores to
+  // complete as well (stores count on vmcnt too).
+  [[maybe_unused]] uint32_t km_pend[NB];
+  [[maybe_unused]] int km_n0 = -1;  // first key of the pending tile, or -1
+  auto flush_keep = [&]() __attribute__((always_inline)) {
+    if constexpr (DROP == 2) {
+      if (km_n0 >= 0) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          ((uint16_t*)p.keep_map)[2 * (keep_map_block((int64_t)b * p.Hq + hq, iw0 >> 5, (km_n0 >> 5) + nb, p.km_nbi,
+                                                      p.km_nbj) + r) + g] = (uint16_t)km_pend[nb];
+        km_n0 = -1;
+      }
+    }
+  };
+
   // Softmax update of one tile; writes P^T packed as the PV B operand.  All
   // in the raw-score domain: a tile that reads the mask adds mask * log2e / c
   // to its raw scores, an edge tile sets the scores it may not see to -inf;
@@ -525,7 +547,8 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
         for (int v = 0; v < 16; ++v) rs += s[nb][v];
       l_run += rs;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
+      for (int nb = 0; nb < NB; ++nb) {
+        uint32_t kw = 0;  // keep bits of this lane's 16 elements of the block (bit v: element v)
 #pragma unroll
         for (int vp = 0; vp < 2; ++vp) {
           // 8-key groups vq = 2vp, 2vp + 1: one Philox call per lane pair
@@ -535,7 +558,7 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
             xa[e] = s[nb][vp * 8 + e];
             xb[e] = s[nb][vp * 8 + 4 + e];
           }
-          dropout_pair(xa, xb, dkey, b * p.Hq + hq, i, n0 + nb * 32 + vp * 16, g);
+          kw |= dropout_pair(xa, xb, dkey, b * p.Hq + hq, i, n0 + nb * 32 + vp * 16, g) << (vp * 8);
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             s[nb][vp * 8 + e] = xa[e];
@@ -545,6 +568,9 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
           // need more registers than the kernel has)
           if constexpr (MASK) __builtin_amdgcn_sched_barrier(0);
         }
+        if constexpr (DROP == 2) km_pend[nb] = kw;
+      }
+      if constexpr (DROP == 2) km_n0 = n0;
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -597,6 +623,7 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
         load_k(kbuf(other) + u * BN * D, T + ks + u);
         load_v(vbuf(other) + u * BN * D, T + ks + u);
       }
+    flush_keep();
     if (t < t_hi && tile_live(t)) {
       const int n0 = t * BN;
       uint16_t* kt = kbuf(slot) + kp * BN * D;
@@ -643,6 +670,7 @@ __global__ __launch_bounds__(NW * 64, (MASK && D == 64) ? 3 : OCC) void attn_fwd
     step(std::false_type{}, std::integral_constant<int, 1>{}, t_lo + ks * (si + 1));
   }
   for (; si < s_hi; ++si) step(std::true_type{}, si & 1, t_lo + ks * si);
+  flush_keep();
 
   if (KS != 1 && ks == 2) {
     // Merge the two key halves of each row group: wavefront 2r+1 hands its
@@ -711,7 +739,8 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
     return launch_kernel(&attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, (F & kFeatMask) != 0,  \
-                                          (F & kFeatDropout) != 0, (F & kFeatQNorm) != 0>,                     \
+                                          (F & kFeatKeepMap) ? 2 : ((F & kFeatDropout) ? 1 : 0),               \
+                                          (F & kFeatQNorm) != 0>,                                              \
                          grid, block, 0, st, p);
     TRINIX_CASE(0)
     TRINIX_CASE(1)
@@ -723,6 +752,18 @@ hipError_t launch_feat(const FwdParams& p, int feat, hipStream_t st) {
     TRINIX_CASE(7)
     default:
       break;
+  }
+  // Dropout writing the keep map: head_dim 64 and 128 (the backward that
+  // reads it)
+  if constexpr (D <= 128) {
+    switch (feat) {
+      TRINIX_CASE((kFeatDropout | kFeatKeepMap))
+      TRINIX_CASE((kFeatDropout | kFeatKeepMap | kFeatAlibi))
+      TRINIX_CASE((kFeatDropout | kFeatKeepMap | kFeatMask))
+      TRINIX_CASE((kFeatDropout | kFeatKeepMap | kFeatAlibi | kFeatMask))
+      default:
+        break;
+    }
   }
   // The fused q RMSNorm is its own instantiation (the other kernels keep
   // their code unchanged): without and with ALiBi, one wavefront per row
@@ -748,7 +789,7 @@ hipError_t launch_feat_plain(const FwdParams& p, int feat, hipStream_t st) {
   switch (feat) {
 #define TRINIX_CASE(F)                                                                                          \
   case F:                                                                                                       \
-    return launch_kernel(&attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, false, false,         \
+    return launch_kernel(&attn_fwd_mfma16<E, D, BN, NW, OCC, KS, (F & kFeatAlibi) != 0, false, 0,             \
                                           (F & kFeatQNorm) != 0>,                                              \
                          grid, block, 0, st, p);
     TRINIX_CASE(0)
@@ -767,9 +808,9 @@ hipError_t launch_feat_plain(const FwdParams& p, int feat, hipStream_t st) {
 template <class E, int D>
 hipError_t launch_feat_split(const FwdParams& p, int feat, hipStream_t st) {
   const dim3 grid((unsigned)p.total_work), block(4 * 64);
-  if (feat == 0) return launch_kernel(&attn_fwd_mfma16<E, D, 64, 4, 2, 0, false, false, false, false>, grid, block, 0, st, p);
+  if (feat == 0) return launch_kernel(&attn_fwd_mfma16<E, D, 64, 4, 2, 0, false, false, 0, false>, grid, block, 0, st, p);
   if (feat == kFeatAlibi)
-    return launch_kernel(&attn_fwd_mfma16<E, D, 64, 4, 2, 0, true, false, false, false>, grid, block, 0, st, p);
+    return launch_kernel(&attn_fwd_mfma16<E, D, 64, 4, 2, 0, true, false, 0, false>, grid, block, 0, st, p);
   return hipErrorNotSupported;
 }
 

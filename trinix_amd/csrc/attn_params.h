@@ -41,6 +41,8 @@ struct FwdParams {
   const uint16_t* qn_w;  // fused q RMSNorm weight (head_dim), or null
   float qn_eps;
   uint16_t* qn_out;  // the normalised q, contiguous (B, Sq, Hq, D), or null
+  uint32_t* keep_map;    // dropout keep bits written for the backward (index_map.h), or null
+  int64_t km_nbi, km_nbj;  // its row / key blocks per (batch, q-head)
   // work items of the per-item key split (Cfg16 ks = 0), longest chain
   // first: row block << 2 | split << 1 | half (plan_split_rows)
   uint8_t row_items[kMaxRowItems];
@@ -112,15 +114,28 @@ __device__ inline DropKey drop_key(const P& p) {
 // (xb), e = 0..3, of row i, ga % 8 == 0, g the lane half (the lane pair
 // l, l + 32 holds row i): p <- keep ? p : 0.  The 1/(1-p) of the kept
 // weights is applied to the output once, in the kernels' epilogues.
-__device__ inline void dropout_pair(float (&xa)[4], float (&xb)[4], const DropKey& dkey, int bh, int i, int ga, int g) {
+// Returns the keep bits: bit e for xa's key e, bit 4 + e for xb's (the
+// lane's elements 4q + e of a 32x32 MFMA result block hold keys
+// 8q + 4g + e of the block, so bits of the two calls of a block, shifted
+// left by 8 * (ga % 32) / 16, give bit v for element v).
+__device__ inline uint32_t dropout_pair(float (&xa)[4], float (&xb)[4], const DropKey& dkey, int bh, int i, int ga,
+                                        int g) {
   uint32_t wa[2], wb[2];
   philox_pair_words((uint32_t)(ga >> 3), (uint32_t)i, (uint32_t)bh, dkey.off_lo, dkey.k0, dkey.k1, g, wa, wb);
+  uint32_t bits = 0;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    xa[e] = keep_field(wa[e >> 1], e & 1, dkey.thresh) ? xa[e] : 0.f;
-    xb[e] = keep_field(wb[e >> 1], e & 1, dkey.thresh) ? xb[e] : 0.f;
+    const bool ka = keep_field(wa[e >> 1], e & 1, dkey.thresh), kb = keep_field(wb[e >> 1], e & 1, dkey.thresh);
+    xa[e] = ka ? xa[e] : 0.f;
+    xb[e] = kb ? xb[e] : 0.f;
+    bits |= (ka ? 1u : 0u) << e;
+    bits |= (kb ? 1u : 0u) << (4 + e);
   }
+  return bits;
 }
+
+// All ones when bit v of keep bits m is set, else 0 (one v_bfe_i32).
+__device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int)(m << (31 - v)) >> 31); }
 
 // Combine a value with the one held by lane l ^ 32 (v_permlane32_swap).
 __device__ inline float xlane_max(float x) {
@@ -146,6 +161,6 @@ hipError_t launch_attn16_f16_d256(const FwdParams& p, Cfg16 cfg, int feat, hipSt
 
 
 // Feature bits of a launch (compile-time flags of the 16-bit kernels).
-enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4, kFeatQNorm = 8 };
+enum : int { kFeatAlibi = 1, kFeatMask = 2, kFeatDropout = 4, kFeatQNorm = 8, kFeatKeepMap = 16 };
 
 }  // namespace trinix

@@ -17,6 +17,7 @@
 #include <cstdint>
 
 #include "common.h"
+#include "index_map.h"
 #include "trinix_attn.h"
 
 namespace {
@@ -40,4 +41,18 @@ extern "C" int trinix_dropout_state_advance(uint64_t* generator, uint64_t* call_
   const hipError_t err = trinix::launch_kernel(&dropout_state_advance_kernel, dim3(1), dim3(64), 0,
                                                (hipStream_t)stream, generator, call_state, increment);
   return err == hipSuccess ? TRINIX_OK : TRINIX_ERR_LAUNCH;
+}
+
+// Size of the keep map a dropout forward writes for its backward
+// (trinix_attn_fwd_args.dropout_keep_map; layout in index_map.h).
+extern "C" int trinix_dropout_keep_map_bytes(int64_t batch, int64_t nheads_q, int64_t seqlen_q, int64_t seqlen_k,
+                                             int64_t* bytes) {
+  if (!bytes) return TRINIX_ERR_NULL_POINTER;
+  if (batch <= 0 || nheads_q <= 0 || seqlen_q <= 0 || seqlen_k <= 0 || seqlen_q >= (1ll << 30) ||
+      seqlen_k >= (1ll << 30) || batch >= (1 << 20) || nheads_q >= (1 << 20))
+    return TRINIX_ERR_BAD_SHAPE;
+  const int64_t blocks = trinix::keep_map_nbi(seqlen_q) * trinix::keep_map_nbj(seqlen_k);
+  if (blocks > (INT64_MAX / 128) / (batch * nheads_q)) return TRINIX_ERR_BAD_SHAPE;
+  *bytes = 128 * batch * nheads_q * blocks;
+  return TRINIX_OK;
 }

@@ -157,6 +157,13 @@ static bool mask_strides_ok(const int64_t st[4], int64_t sq, int64_t sk) {
   return mask_key_stride_ok(st[3], sk);
 }
 
+// A dropout keep map goes with dropout, the 16-bit kernels at head_dim 64
+// or 128 (the MFMA backward that reads it), and a 16-byte aligned buffer.
+static bool keep_map_ok(const void* map, float dropout_p, int32_t dtype, int64_t head_dim) {
+  return dropout_p > 0.f && (dtype == TRINIX_BF16 || dtype == TRINIX_F16) && (head_dim == 64 || head_dim == 128) &&
+         aligned16(map);
+}
+
 int validate_fwd_args(const trinix_attn_fwd_args* a) {
   if (!a) return TRINIX_ERR_NULL_POINTER;
   const int esize = a->dtype == TRINIX_F32 ? 4 : 2;
@@ -189,6 +196,8 @@ int validate_fwd_args(const trinix_attn_fwd_args* a) {
       (!aligned16(a->rope_cos) || !aligned16(a->rope_sin) || a->rope_stride % 8 != 0))
     return TRINIX_ERR_BAD_STRIDE;
   if (a->q_norm_out && (!a->q_norm_weight || !aligned16(a->q_norm_out))) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->dropout_keep_map && !keep_map_ok(a->dropout_keep_map, a->dropout_p, a->dtype, a->head_dim))
+    return TRINIX_ERR_BAD_ARGUMENT;
   if (a->q_norm_weight) {
     if (esize != 2) return TRINIX_ERR_BAD_DTYPE;
     if (a->mask || a->dropout_p > 0.f) return TRINIX_ERR_BAD_ARGUMENT;
@@ -205,6 +214,8 @@ int validate_bwd_args(const trinix_attn_bwd_args* a) {
   if (a->head_dim != 64 && a->head_dim != 128 && a->head_dim != 256) return TRINIX_ERR_BAD_HEAD_DIM;
   if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f)) return TRINIX_ERR_BAD_ARGUMENT;
   if (a->dropout_state && ((uintptr_t)a->dropout_state & 7)) return TRINIX_ERR_BAD_ARGUMENT;
+  if (a->dropout_keep_map && !keep_map_ok(a->dropout_keep_map, a->dropout_p, a->dtype, a->head_dim))
+    return TRINIX_ERR_BAD_ARGUMENT;
   if (a->batch <= 0 || a->seqlen_q <= 0 || a->seqlen_k <= 0 || a->nheads_q <= 0 || a->nheads_kv <= 0 ||
       a->nheads_q % a->nheads_kv != 0)
     return TRINIX_ERR_BAD_SHAPE;

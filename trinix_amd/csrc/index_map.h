@@ -243,6 +243,23 @@ __host__ __device__ inline void bwd_key_tiles(int m0, int BM, int Sq, int Sk, in
   t_hi = hi > lo ? (int)((hi + BN - 1) / BN) : t_lo;
 }
 
+// ---- dropout keep map ---------------------------------------------------------
+// The keep decisions of a dropout forward, one bit per (row i, key j) of
+// each (batch, q-head) bh, stored so that the backward reads them instead of
+// regenerating them.  Blocks of 32 rows x 32 keys, KM_NBI row blocks by
+// KM_NBJ key blocks per bh, padded to whole 64-row and 128-key tiles so that
+// every tile copy of the backward stays inside the map.  A block is 32
+// uint32 words, word i % 32 holding row i; its bit 16h + 4q + e is key
+// 8q + 4h + e of the block (kept = 1), h = 0, 1, q, e = 0..3: the order in
+// which a lane pair of the kernels holds a row's 32 keys (lane half h,
+// element 4q + e).  The blocks of one row block are consecutive in j.
+__host__ __device__ inline int64_t keep_map_nbi(int64_t Sq) { return 2 * ((Sq + 63) / 64); }
+__host__ __device__ inline int64_t keep_map_nbj(int64_t Sk) { return 4 * ((Sk + 127) / 128); }
+// Word index of the first word of block (bi, bj) of bh.
+__host__ __device__ inline int64_t keep_map_block(int64_t bh, int64_t bi, int64_t bj, int64_t nbi, int64_t nbj) {
+  return ((bh * nbi + bi) * nbj + bj) * 32;
+}
+
 // ---- split-KV decode (attn_decode16) --------------------------------------
 // Work item of workgroup `blk`: 16 packed rows (row group rg), one key chunk,
 // (batch, kv-head) bh.

@@ -24,6 +24,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from typing import Optional, Tuple
 
 import torch
@@ -233,6 +234,34 @@ def dropout_generator(device: torch.device) -> torch.Tensor:
         gen = torch.tensor([seed, 1 << 32], dtype=torch.int64, device=device)
         _DROPOUT_GENERATORS[device] = gen
     return gen
+
+
+# Dropout keep map: a forward with dropout that keeps state for a backward
+# writes its keep decisions (one bit per (row, key)) so that the backward
+# reads them instead of regenerating them from Philox (about 0.3 ms of the
+# backward at B=1, S=8192, 32 heads, D=128).  The map takes
+# 128*B*H*2*ceil(Sq/64)*4*ceil(Sk/128) bytes (1/8 byte per (row, key); the
+# eager path keeps a mask of one element per (row, key)): 268 MB at that
+# shape.  Calls whose map would exceed 1/32 of the device's memory regenerate
+# instead; TRINIX_DROPOUT_KEEP_MAP=0 / 1 forces either way.
+_KEEP_MAP_LIMIT: dict = {}
+
+
+def _keep_map_bytes(device: torch.device, B: int, H: int, Sq: int, Sk: int) -> int:
+    mode = os.environ.get("TRINIX_DROPOUT_KEEP_MAP", "")
+    if mode == "0":
+        return 0
+    n = ctypes.c_int64(0)
+    nat.check(nat.load_library().trinix_dropout_keep_map_bytes(B, H, Sq, Sk, ctypes.byref(n)),
+              "trinix_dropout_keep_map_bytes")
+    if mode != "1":
+        lim = _KEEP_MAP_LIMIT.get(device)
+        if lim is None:
+            lim = torch.cuda.get_device_properties(device).total_memory // 32
+            _KEEP_MAP_LIMIT[device] = lim
+        if n.value > lim:
+            return 0
+    return n.value
 
 
 # ---------------------------------------------------------------------------
@@ -447,7 +476,7 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             args.mask_blockmap = bmap.data_ptr()
             args.blockmap_stride = nat.int64x2(bst)
 
-    drop_state = None
+    drop_state = keep_map = None
     if dropout_p > 0.0:
         args.dropout_p = float(dropout_p)
         if torch.cuda.is_current_stream_capturing():
@@ -471,6 +500,12 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             # Seed from torch's CPU generator: no device->host sync.
             args.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
             args.dropout_offset = 0
+        if keep_state and q.dtype != torch.float32 and d_kernel in (64, 128):
+            km_bytes = _keep_map_bytes(device, B, H, Sq, Sk)
+            if km_bytes:
+                keep_map = torch.empty(km_bytes, dtype=torch.uint8, device=device)
+                args.dropout_keep_map = keep_map.data_ptr()
+                keep.append(keep_map)
 
     if rotary_cos is not None:
         cos = rotary_cos.to(device=device, dtype=q.dtype)
@@ -532,7 +567,7 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
         state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),
                      window=window_size, D=D, d_kernel=d_kernel, keep=keep, args=args,
                      dropout=(float(args.dropout_p), int(args.dropout_seed), int(args.dropout_offset)),
-                     dropout_state=drop_state)
+                     dropout_state=drop_state, keep_map=keep_map)
     if d_kernel != D:
         out = out[..., :D].contiguous()
     return out, lse, state
@@ -569,6 +604,8 @@ def _backward(state, dout):
     a.dropout_p, a.dropout_seed, a.dropout_offset = state["dropout"]
     if state["dropout_state"] is not None:
         a.dropout_state = state["dropout_state"].data_ptr()
+    if state["keep_map"] is not None:
+        a.dropout_keep_map = state["keep_map"].data_ptr()
     rc = nat.load_library().trinix_attn_bwd(ctypes.byref(a), current_stream_ptr(qk.device))
     nat.check(rc, "trinix_attn_bwd")
     if dkrn != D:
