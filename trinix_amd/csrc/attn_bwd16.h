@@ -245,12 +245,14 @@ __device__ inline uint32_t transpose_keep_block(uint32_t a, int lane) {
 // stage B's item, the item being loaded) and P through 2; one barrier per
 // item orders all of it.  The loop runs six steps per trip so that every slot
 // index is a compile-time constant (LDS addresses as immediate offsets).
-// With dropout (DROP), stage A regenerates the keep bits of its sub-tile,
-// takes dV^T += dO^T (keep ? P : 0), and hands the bits to stage B through
-// LDS next to P; stage B takes dZ' = P (keep dP - delta (1-p)), the delta
-// kernel having scaled delta = rowsum(dO*O) by 1-p.  The 1/(1-p) of
-// Pd = keep P/(1-p) and of dZ = P (keep dP/(1-p) - delta) = dZ'/(1-p) is
-// applied once per output element in the epilogue.
+// With dropout (DROP = 1: regenerated from Philox; DROP = 2: the forward's
+// keep map, whose words of the item's rows are copied to LDS with its tiles
+// and transposed in registers, transpose_keep_block), stage A takes the keep
+// bits of its sub-tile, dV^T += dO^T (keep ? P : 0), and hands the bits to
+// stage B through LDS next to P; stage B takes dZ' = P (keep dP - delta
+// (1-p)), the delta kernel having scaled delta = rowsum(dO*O) by 1-p.  The
+// 1/(1-p) of Pd = keep P/(1-p) and of dZ = P (keep dP/(1-p) - delta) =
+// dZ'/(1-p) is applied once per output element in the epilogue.
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, int DROP>
 __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
@@ -650,8 +652,10 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
 // dQ^T += K^T dZ^T with K^T from LDS transpose reads.  With dropout (DROP)
 // dZ' = P (keep dP - delta (1-p)) (delta scaled by the delta kernel) and
 // the 1/(1-p) of dZ = dZ'/(1-p) applied in the epilogue; the keep bits are
-// drawn as the forward draws them: the two lanes of a row share the calls
-// of 8-key group pairs (philox_pair_words).
+// drawn as the forward draws them (DROP = 1: the two lanes of a row share
+// the calls of 8-key group pairs, philox_pair_words) or read from the
+// forward's keep map (DROP = 2: each wavefront copies its rows' words of a
+// key tile to LDS with the tile).
 // ---------------------------------------------------------------------------
 template <class E, int D, bool ALIBI, bool MASK, int DROP, int NW, int BN>
 __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
