@@ -21,7 +21,8 @@ STUB = r"""
 #include <string.h>
 #include "trinix_attn.h"
 static trinix_attn_fwd_args last_fwd, last_split;
-static int n_fwd, n_split, n_rope, n_plan;
+static trinix_attn_bwd_args last_bwd;
+static int n_fwd, n_split, n_rope, n_plan, n_bwd;
 static int64_t last_rope[16];
 static int64_t split_ws;
 int trinix_abi_version(void) { return %(abi)d; }
@@ -40,7 +41,12 @@ int trinix_rope_apply(const void* x, const int64_t* xs, void* out, const int64_t
                    os[3], B * 1000003 + S, H * 1000003 + D, dt, (int64_t)(intptr_t)c ^ (int64_t)(intptr_t)sn,
                    cst * 1000003 + rows, (int64_t)(intptr_t)pos};
   memcpy(last_rope, v, sizeof v); ++n_rope; return 0; }
-int stub_counts(int* out) { out[0] = n_fwd; out[1] = n_split; out[2] = n_rope; out[3] = n_plan; return 0; }
+int trinix_attn_bwd(const trinix_attn_bwd_args* a, void* s) { (void)s; last_bwd = *a; ++n_bwd; return 0; }
+int trinix_dropout_keep_map_bytes(int64_t b, int64_t h, int64_t sq, int64_t sk, int64_t* n) {
+  *n = 128 * b * h * 2 * ((sq + 63) / 64) * 4 * ((sk + 127) / 128); return 0; }
+int stub_counts(int* out) { out[0] = n_fwd; out[1] = n_split; out[2] = n_rope; out[3] = n_plan; out[4] = n_bwd;
+  return 0; }
+const trinix_attn_bwd_args* stub_last_bwd(void) { return &last_bwd; }
 const trinix_attn_fwd_args* stub_last_fwd(void) { return &last_fwd; }
 const trinix_attn_fwd_args* stub_last_split(void) { return &last_split; }
 const int64_t* stub_last_rope(void) { return last_rope; }
@@ -49,7 +55,8 @@ int64_t stub_split_ws(void) { return split_ws; }
 # entry points the stub does not record: they only have to exist
 OTHERS = [n for n in nat.SIGNATURES if n not in (
     "trinix_abi_version", "trinix_attn_is_available", "trinix_status_string", "trinix_attn_fwd",
-    "trinix_attn_fwd_splitkv_plan", "trinix_attn_fwd_splitkv", "trinix_rope_apply")]
+    "trinix_attn_fwd_splitkv_plan", "trinix_attn_fwd_splitkv", "trinix_rope_apply", "trinix_attn_bwd",
+    "trinix_dropout_keep_map_bytes")]
 
 
 @pytest.fixture(scope="module")
@@ -75,6 +82,7 @@ def stub(stub_path, monkeypatch):
     lib.stub_last_split.restype = ctypes.POINTER(nat.AttnFwdArgs)
     lib.stub_last_rope.restype = ctypes.POINTER(ctypes.c_int64 * 16)
     lib.stub_split_ws.restype = ctypes.c_int64
+    lib.stub_last_bwd.restype = ctypes.POINTER(nat.AttnBwdArgs)
     monkeypatch.setattr(nat, "_lib", lib)
     monkeypatch.setattr(torch.Tensor, "is_cuda", property(lambda self: True))
     monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
@@ -82,11 +90,13 @@ def stub(stub_path, monkeypatch):
     monkeypatch.setattr(ak, "current_stream_ptr", lambda dev: 0)
     monkeypatch.setattr(rk, "current_stream_ptr", lambda dev: 0)
     monkeypatch.setattr(ak, "_LAUNCHES", {})
+    monkeypatch.setattr(ak, "_TRAIN_LAUNCHES", {})
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
     return lib
 
 
 def counts(lib):
-    c = (ctypes.c_int * 4)()
+    c = (ctypes.c_int * 5)()
     lib.stub_counts(c)
     return list(c)
 
@@ -237,3 +247,86 @@ def test_calls_with_other_features_are_not_cached(stub, feature):
     except Exception:
         pass  # the stub has no mask pre-pass output to return; only the cache matters here
     assert len(ak._LAUNCHES) == 0
+
+
+BWD_PTRS = ("q", "k", "v", "out", "dout", "lse", "delta", "dq", "dk", "dv", "dropout_keep_map")
+
+
+def bwd_bytes(a, zero=BWD_PTRS + ("dropout_seed",)):
+    b = nat.AttnBwdArgs.from_buffer_copy(a)
+    for f in zero:
+        setattr(b, f, 0 if f == "dropout_seed" else None)
+    return bytes(b)
+
+
+def _train_step(q, k, v, do, **kw):
+    from trinix_amd import triton_attn_func
+
+    ts = [t.detach().clone().requires_grad_(True) for t in (q, k, v)]
+    out = triton_attn_func(*ts, **kw)
+    out.backward(do)
+    return ts, out
+
+
+@pytest.mark.parametrize("dropout", [0.0, 0.2])
+def test_training_launches_are_cached(stub, monkeypatch, dropout):
+    """A differentiable call of a cached layout hands the forward and the
+    backward the full path's structs, its own pointers and, with dropout, a
+    fresh seed shared by its forward and backward (and its keep map)."""
+    monkeypatch.setenv("TRINIX_DROPOUT_KEEP_MAP", "1")
+    q, k, v = qkv(S=70, D=128)
+    do = torch.randn_like(q)
+    kw = dict(causal=True, dropout_p=dropout)
+    c0 = counts(stub)
+    _train_step(q, k, v, do, **kw)
+    n0 = counts(stub)
+    assert n0[0] == c0[0] + 1 and n0[4] == c0[4] + 1 and len(ak._TRAIN_LAUNCHES) == 1
+    fwd_full = struct_bytes(stub.stub_last_fwd().contents, zero=("q", "k", "v", "out", "lse", "dropout_keep_map"))
+    f_full = nat.AttnFwdArgs.from_buffer_copy(stub.stub_last_fwd().contents)
+    b_full = nat.AttnBwdArgs.from_buffer_copy(stub.stub_last_bwd().contents)
+    ent = ak._TRAIN_LAUNCHES[next(iter(ak._TRAIN_LAUNCHES))]
+    assert ent.bwd is not None
+    seeds = {f_full.dropout_seed}
+    for rep in range(2):
+        q2, k2, v2 = qkv(S=70, D=128, seed=10 + rep)
+        ts, out = _train_step(q2, k2, v2, do, **kw)
+        assert counts(stub)[0] == n0[0] + rep + 1 and counts(stub)[4] == n0[4] + rep + 1
+        f = nat.AttnFwdArgs.from_buffer_copy(stub.stub_last_fwd().contents)
+        b = nat.AttnBwdArgs.from_buffer_copy(stub.stub_last_bwd().contents)
+        cmp = nat.AttnFwdArgs.from_buffer_copy(f)
+        cmp.dropout_seed = f_full.dropout_seed
+        assert struct_bytes(cmp, zero=("q", "k", "v", "out", "lse", "dropout_keep_map")) == fwd_full
+        b_cmp = nat.AttnBwdArgs.from_buffer_copy(b)
+        assert bwd_bytes(b_cmp) == bwd_bytes(b_full)
+        assert (f.q, f.k, f.v) == tuple(t.data_ptr() for t in ts) and f.out == out.data_ptr()
+        assert (b.q, b.k, b.v, b.out, b.lse) == (f.q, f.k, f.v, f.out, f.lse)
+        assert b.dq == ts[0].grad.data_ptr() and b.dk == ts[1].grad.data_ptr() and b.dv == ts[2].grad.data_ptr()
+        assert b.dropout_seed == f.dropout_seed and b.dropout_keep_map == f.dropout_keep_map
+        if dropout:
+            assert f.dropout_keep_map and f.dropout_p == pytest.approx(dropout)
+            seeds.add(f.dropout_seed)
+        else:
+            assert not f.dropout_keep_map and f.dropout_seed == 0
+    assert len(seeds) == (3 if dropout else 1)
+    assert len(ak._TRAIN_LAUNCHES) == 1
+
+
+def test_training_cache_follows_the_keep_map_switch(stub, monkeypatch):
+    q, k, v = qkv(S=70, D=64)
+    do = torch.randn_like(q)
+    for mode, want in (("1", True), ("0", False), ("1", True), ("0", False)):
+        monkeypatch.setenv("TRINIX_DROPOUT_KEEP_MAP", mode)
+        _train_step(q, k, v, do, causal=True, dropout_p=0.1)
+        f = stub.stub_last_fwd().contents
+        b = stub.stub_last_bwd().contents
+        assert bool(f.dropout_keep_map) == want and b.dropout_keep_map == f.dropout_keep_map
+    assert len(ak._TRAIN_LAUNCHES) == 2
+
+
+def test_training_with_alibi_or_mask_is_not_cached(stub, monkeypatch):
+    q, k, v = qkv(S=70, D=64)
+    do = torch.randn_like(q)
+    c0 = counts(stub)
+    _train_step(q, k, v, do, alibi_slopes=torch.ones(4))
+    _train_step(q, k, v, do, attn_mask=torch.zeros(70, 70))
+    assert len(ak._TRAIN_LAUNCHES) == 0 and counts(stub)[4] == c0[4] + 2

@@ -343,6 +343,67 @@ def _launch_cached(key, q, k, v, rotary_cos, rotary_sin):
     return out
 
 
+# Training launches.  A differentiable call (the forward keeps state for the
+# backward) without mask, ALiBi, q-norm or fused rotary tables, whose
+# operands the kernels read in place, is cached the same way: the forward's
+# argument template (its lse written) and, once the first backward of the
+# layout has run, the backward's template.  Dropout calls draw their seed
+# (and keep map) per call as on the full path.
+class _TrainLaunch:
+    __slots__ = ("fwd", "bwd", "out_shape", "lse_shape", "dtype", "device", "align", "km_bytes", "do_stride",
+                 "dk_shape")
+
+    def __init__(self, fwd, out_shape, lse_shape, dtype, device, align, km_bytes, dk_shape):
+        self.fwd = fwd                # AttnFwdArgs with null data pointers and seed
+        self.bwd = None               # AttnBwdArgs template after the first backward, or None
+        self.out_shape = out_shape
+        self.lse_shape = lse_shape
+        self.dtype = dtype
+        self.device = device
+        self.align = align
+        self.km_bytes = km_bytes      # dropout keep map bytes (0: none)
+        self.do_stride = None         # dout strides the backward template was built for
+        self.dk_shape = dk_shape      # shape of k (and of dk, dv)
+
+
+_TRAIN_LAUNCHES: dict = {}
+
+
+def _train_key(q, k, v, causal, scale, dropout_p, window_size, return_lse):
+    key = _launch_key(q, k, v, causal, scale, window_size, None, None, False)
+    if key is None:
+        return None
+    return key, float(dropout_p), bool(return_lse), os.environ.get("TRINIX_DROPOUT_KEEP_MAP", "")
+
+
+def _train_cached(tkey, q, k, v):
+    """(out, lse, state) of a differentiable call whose layout has a cached
+    training launch, or None."""
+    ent = _TRAIN_LAUNCHES.get(tkey)
+    if ent is None:
+        return None
+    qp, kp, vp = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    if (qp | kp | vp) % ent.align:
+        return None
+    a = nat.AttnFwdArgs.from_buffer_copy(ent.fwd)
+    keep_map = None
+    if a.dropout_p > 0.0:
+        if torch.cuda.is_current_stream_capturing():
+            return None  # the device-side dropout state of the full path
+        a.dropout_seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+        if ent.km_bytes:
+            keep_map = torch.empty(ent.km_bytes, dtype=torch.uint8, device=ent.device)
+            a.dropout_keep_map = keep_map.data_ptr()
+    out = torch.empty(ent.out_shape, dtype=ent.dtype, device=ent.device)
+    lse = torch.empty(ent.lse_shape, dtype=torch.float32, device=ent.device)
+    a.q, a.k, a.v, a.out, a.lse = qp, kp, vp, out.data_ptr(), lse.data_ptr()
+    nat.check(nat.load_library().trinix_attn_fwd(ctypes.byref(a), current_stream_ptr(ent.device)), "trinix_attn_fwd")
+    D = ent.out_shape[-1]
+    state = dict(q=q, k=k, v=v, out=out, lse=lse, D=D, d_kernel=D, args=a, launch=ent,
+                 dropout=(float(a.dropout_p), int(a.dropout_seed), 0), dropout_state=None, keep_map=keep_map)
+    return out, lse, state
+
+
 def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, rotary_cos, rotary_sin,
              rotary_k, return_lse, use_blockmap, keep_state=False, q_norm_weight=None, q_norm_eps=1e-6,
              q_norm_out=None):
@@ -357,6 +418,14 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
             out = _launch_cached(key, q, k, v, rotary_cos, rotary_sin)
             if out is not None:
                 return out, None, None
+    tkey = None
+    if (keep_state and attn_mask is None and alibi_slopes is None and q_norm_weight is None and rotary_cos is None
+            and rotary_sin is None):
+        tkey = _train_key(q, k, v, causal, scale, dropout_p, window_size, return_lse)
+        if tkey is not None:
+            res = _train_cached(tkey, q, k, v)
+            if res is not None:
+                return res
     q_in, k_in, v_in, cos_in, sin_in = q, k, v, rotary_cos, rotary_sin
     rope_tpl = None
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
@@ -564,8 +633,18 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
                                      rope_tpl[:-1] if rope_tpl is not None else None, split_bytes)
     state = None
     if keep_state:
-        state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, scale=float(scale), causal=bool(causal),
-                     window=window_size, D=D, d_kernel=d_kernel, keep=keep, args=args,
+        ent = None
+        if (tkey is not None and d_kernel == D and qk is q_in and kk is k_in and vk is v_in and drop_state is None
+                and q.dtype != torch.float32 and not launched):
+            tpl = nat.AttnFwdArgs.from_buffer_copy(args)
+            tpl.q = tpl.k = tpl.v = tpl.out = tpl.lse = tpl.dropout_keep_map = None
+            tpl.dropout_seed = 0
+            if len(_TRAIN_LAUNCHES) >= _MAX_LAUNCHES:
+                _TRAIN_LAUNCHES.clear()
+            ent = _TrainLaunch(tpl, tuple(out.shape), tuple(lse.shape), q.dtype, device, 16,
+                               keep_map.numel() if keep_map is not None else 0, tuple(kk.shape))
+            _TRAIN_LAUNCHES[tkey] = ent
+        state = dict(q=qk, k=kk, v=vk, out=out, lse=lse, D=D, d_kernel=d_kernel, keep=keep, args=args, launch=ent,
                      dropout=(float(args.dropout_p), int(args.dropout_seed), int(args.dropout_offset)),
                      dropout_state=drop_state, keep_map=keep_map)
     if d_kernel != D:
@@ -576,6 +655,11 @@ def _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_sl
 def _backward(state, dout):
     """Launch ``trinix_attn_bwd`` for a forward run with ``keep_state``;
     returns (dq, dk, dv) at the caller's head_dim, in the input dtype."""
+    ent = state.get("launch")
+    if ent is not None and ent.bwd is not None:
+        res = _backward_cached(state, ent, dout)
+        if res is not None:
+            return res
     qk, kk, vk, out, lse = state["q"], state["k"], state["v"], state["out"], state["lse"]
     fa = state["args"]
     D, dkrn = state["D"], state["d_kernel"]
@@ -608,8 +692,37 @@ def _backward(state, dout):
         a.dropout_keep_map = state["keep_map"].data_ptr()
     rc = nat.load_library().trinix_attn_bwd(ctypes.byref(a), current_stream_ptr(qk.device))
     nat.check(rc, "trinix_attn_bwd")
+    if ent is not None and ent.bwd is None and do is dout and state["dropout_state"] is None:
+        tpl = nat.AttnBwdArgs.from_buffer_copy(a)
+        tpl.q = tpl.k = tpl.v = tpl.out = tpl.dout = tpl.lse = tpl.delta = tpl.dq = tpl.dk = tpl.dv = None
+        tpl.dropout_keep_map = None
+        tpl.dropout_seed = 0
+        ent.do_stride = tuple(do.stride())
+        ent.bwd = tpl
     if dkrn != D:
         dq, dk, dv = dq[..., :D], dk[..., :D], dv[..., :D]
+    return dq, dk, dv
+
+
+def _backward_cached(state, ent, dout):
+    """(dq, dk, dv) through the layout's backward template, or None when
+    dout is not laid out as the template's."""
+    if dout.dtype != ent.dtype or dout.stride() != ent.do_stride or dout.data_ptr() % ent.align:
+        return None
+    dev = ent.device
+    a = nat.AttnBwdArgs.from_buffer_copy(ent.bwd)
+    dq = torch.empty(ent.out_shape, dtype=ent.dtype, device=dev)
+    dk = torch.empty(ent.dk_shape, dtype=ent.dtype, device=dev)
+    dv = torch.empty(ent.dk_shape, dtype=ent.dtype, device=dev)
+    delta = torch.empty(ent.lse_shape, dtype=torch.float32, device=dev)
+    a.q, a.k, a.v = state["q"].data_ptr(), state["k"].data_ptr(), state["v"].data_ptr()
+    a.out, a.dout, a.lse, a.delta = state["out"].data_ptr(), dout.data_ptr(), state["lse"].data_ptr(), delta.data_ptr()
+    a.dq, a.dk, a.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    if a.dropout_p > 0.0:
+        a.dropout_seed = state["dropout"][1]
+        if state["keep_map"] is not None:
+            a.dropout_keep_map = state["keep_map"].data_ptr()
+    nat.check(nat.load_library().trinix_attn_bwd(ctypes.byref(a), current_stream_ptr(dev)), "trinix_attn_bwd")
     return dq, dk, dv
 
 
