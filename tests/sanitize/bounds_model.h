@@ -270,7 +270,7 @@ inline void model_bwd16(Report& R, const trinix_attn_bwd_args& a, const BwdPlan&
   const bool all = nkv <= item_limit;
   std::vector<uint8_t> seen(all ? (size_t)nkv : 0), seen_key(all ? (size_t)B * Hkv * Sk : 0);
   for (int64_t blk : sample(nkv, all ? nkv : 0)) {
-    const KvItem it = bwd_kv_item((int)blk, B, Hkv, pl.num_kblk);
+    const KvItem it = bwd_kv_item((int)blk, B, Hkv, pl.num_kblk, a.causal != 0);
     if (!R.expect(it.b >= 0 && it.b < B && it.hkv >= 0 && it.hkv < Hkv && it.kblk >= 0 && it.kblk < pl.num_kblk,
                   "dkdv item", "block %lld out of range", blk))
       continue;

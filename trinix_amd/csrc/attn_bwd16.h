@@ -278,7 +278,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   const int kg = wave % NG;
   const int g = lane >> 5;
 
-  const KvItem wi = bwd_kv_item((int)blockIdx.x, p.B, p.Hkv, p.num_kblk);  // (index_map.h)
+  const KvItem wi = bwd_kv_item((int)blockIdx.x, p.B, p.Hkv, p.num_kblk, p.causal != 0);  // (index_map.h)
   const int kblk = wi.kblk, hkv = wi.hkv, b = wi.b;
   const int kb0 = kblk * BK;
   const int j0 = kb0 + kg * 32;

@@ -192,13 +192,28 @@ __host__ __device__ inline void band_offsets(bool causal, bool has_window, int64
 }
 
 // dK/dV: work item (batch, kv-head, block of BK keys) of workgroup `blk`.
+// Each XCD owns whole (batch, kv-head) groups, whose Q / dO tiles it then
+// reads from its own L2.  Causal: low key blocks see the most queries; when
+// the groups split evenly over the XCDs, an XCD dispatches the key blocks of
+// all its groups in ascending order (longest first), so that the short
+// blocks fill in behind the long ones.
 struct KvItem {
   int b, hkv, kblk;
 };
-__host__ __device__ inline KvItem bwd_kv_item(int blk, int B, int Hkv, int num_kblk) {
-  int w = xcd_remap(blk, B * Hkv * num_kblk);
+__host__ __device__ inline KvItem bwd_kv_item(int blk, int B, int Hkv, int num_kblk, bool causal) {
   KvItem it;
-  it.kblk = w % num_kblk;  // causal: low key blocks see the most queries, and run first
+  const int groups = B * Hkv;
+  if (causal && groups % kXcds == 0) {
+    const int xcd = blk % kXcds, j = blk / kXcds;  // j: dispatch order in the XCD
+    const int ng = groups / kXcds;
+    it.kblk = j / ng;
+    const int hg = xcd * ng + j % ng;
+    it.hkv = hg % Hkv;
+    it.b = hg / Hkv;
+    return it;
+  }
+  int w = xcd_remap(blk, groups * num_kblk);
+  it.kblk = w % num_kblk;
   w /= num_kblk;
   it.hkv = w % Hkv;
   it.b = w / Hkv;
