@@ -159,3 +159,29 @@ def test_gradients_through_the_map_equal_the_regenerated_mask(case, monkeypatch)
     assert used[-1] == 0
     for name, a, b in zip(("out", "dq", "dk", "dv"), with_map, regen):
         assert torch.equal(a, b), name
+
+
+def test_a_forward_without_backward_frees_its_buffers_at_once():
+    """Dropping the output of a differentiable call without running its
+    backward frees the output, the lse and the keep map at once (no
+    reference cycle through the autograd node), with the cycle collector
+    off."""
+    import gc
+
+    q, k, v = (torch.randn(1, 1024, 4, 128, device=DEV, dtype=torch.bfloat16).requires_grad_(True) for _ in range(3))
+    for p in (0.0, 0.1):  # warm-up: the launch caches and the device's dropout generator
+        triton_attn_func(q, k, v, causal=True, dropout_p=p).sum().backward()
+    q.grad = k.grad = v.grad = None
+    torch.cuda.synchronize()
+    gc.collect()
+    gc.disable()
+    try:
+        base = torch.cuda.memory_allocated()
+        for p in (0.0, 0.1):
+            out = triton_attn_func(q, k, v, causal=True, dropout_p=p)
+            held = torch.cuda.memory_allocated() - base
+            assert held >= out.numel() * out.element_size()
+            del out
+            assert torch.cuda.memory_allocated() == base, (p, held)
+    finally:
+        gc.enable()

@@ -726,6 +726,29 @@ def _backward_cached(state, ent, dout):
     return dq, dk, dv
 
 
+def _save_output(ctx, state, out, *tensors):
+    """Keep the forward's state on ctx.  The returned output, when the state
+    holds that very tensor, is saved through autograd instead
+    (save_for_backward, after ``tensors``): a reference to it from the node
+    that produced it would form a cycle (output -> node -> state -> output),
+    so a forward whose output is dropped without a backward would hold its
+    buffers (output, lse, dropout keep map) until Python's cycle collector
+    runs."""
+    if state["out"] is out:
+        state["out"] = None
+        ctx.save_for_backward(*tensors, out)
+    else:
+        ctx.save_for_backward(*tensors)
+    ctx.state = state
+
+
+def _saved_state(ctx, n_before=0):
+    state = ctx.state
+    if state["out"] is None:
+        state["out"] = ctx.saved_tensors[n_before]
+    return state
+
+
 class _HipAttnFunction(torch.autograd.Function):
     """Differentiable attention: ``trinix_attn_fwd`` forward (keeping the
     log-sum-exp) and ``trinix_attn_bwd`` backward.  RoPE of q (and of k when
@@ -745,7 +768,7 @@ class _HipAttnFunction(torch.autograd.Function):
             ctx.rope = (rotary_cos, rotary_sin, rotary_k)
         out, lse, state = _forward(q, k, v, attn_mask, causal, scale, dropout_p, window_size, alibi_slopes, None,
                                    None, True, True, True, keep_state=True)
-        ctx.state = state
+        _save_output(ctx, state, out)
         if return_lse:
             ctx.mark_non_differentiable(lse)
             return out, lse
@@ -753,7 +776,7 @@ class _HipAttnFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, *unused):
-        dq, dk, dv = _backward(ctx.state, dout.contiguous())
+        dq, dk, dv = _backward(_saved_state(ctx), dout.contiguous())
         ctx.state = None
         if ctx.rope is not None:
             from .rope_kernel import rope_apply
@@ -789,9 +812,8 @@ class _HipAttnQNormFunction(torch.autograd.Function):
                                  rotary_sin, False, True, True, keep_state=True, q_norm_weight=w, q_norm_eps=eps,
                                  q_norm_out=qn)
         state["q"] = qn  # the backward's q: the one attended with
-        ctx.state = state
         c, s, _ = _tables(qc, rotary_cos, rotary_sin, None)
-        ctx.save_for_backward(qc, w, c, s)
+        _save_output(ctx, state, out, qc, w, c, s)
         ctx.eps = float(eps)
         ctx.rope_k = (rotary_cos, rotary_sin) if rotary_cos is not None and rotary_k else None
         return out
@@ -802,8 +824,8 @@ class _HipAttnQNormFunction(torch.autograd.Function):
         from .qk_norm_kernel import _backward as qk_norm_backward
         from .rope_kernel import rope_apply
 
-        qc, w, c, s = ctx.saved_tensors
-        dqn, dk, dv = _backward(ctx.state, dout.contiguous())
+        qc, w, c, s = ctx.saved_tensors[:4]
+        dqn, dk, dv = _backward(_saved_state(ctx, 4), dout.contiguous())
         ctx.state = None
         dq, dw, _ = qk_norm_backward(qc, dqn, w, ctx.eps, c, s, None, NORM_RMS)
         if ctx.rope_k is not None:
