@@ -100,6 +100,10 @@ typedef enum trinix_dtype {
  *   hkv = hq / (nheads_q / nheads_kv)   (GQA/MQA without repeating KV)
  *   lse[b,hq,i] = log(sum_j exp(s[i,j]))  (natural log; optional)
  * Rows with no allowed key give NaN, as softmax over all -inf does.
+ * bf16/fp16 calls without dropout sum the probabilities as rounded to the
+ * input dtype for the P @ V product (the weights out is normalised by), so
+ * their lse is within one unit roundoff of that dtype (2^-8 bf16, 2^-11
+ * fp16) of the exact value; fp32, dropout and split-KV calls sum in fp32.
  */
 typedef struct trinix_attn_fwd_args {
   const void* q;        /* (B, Sq, Hq, D)  */

@@ -515,6 +515,69 @@ def test_lse_output():
     assert torch.allclose(lse.cpu().double(), ref, atol=1e-4, rtol=1e-5)
 
 
+LSE16_CASES = [
+    # (B, Sq, Sk, H, Hkv, D, dtype, kwargs): short causal rows (few keys, so
+    # the rounding of P is not averaged out), long rows, ALiBi with a window,
+    # head_dim 256, and a split-KV decode call (which sums fp32 P)
+    (1, 200, 200, 4, 2, 64, torch.bfloat16, dict(causal=True)),
+    (2, 130, 700, 2, 2, 128, torch.float16, dict()),
+    (1, 256, 256, 4, 4, 128, torch.bfloat16, dict(alibi_slopes=orc.alibi_slopes(4), window_size=(40, 10))),
+    (1, 96, 96, 2, 1, 256, torch.float16, dict(causal=True, softmax_scale=0.3)),
+    (2, 4, 3000, 8, 2, 128, torch.bfloat16, dict()),
+]
+
+
+@pytest.mark.parametrize("case", range(len(LSE16_CASES)))
+def test_lse_output_16bit_within_one_unit_roundoff(case):
+    """bf16/fp16 lse against the fp64 log-sum-exp of the same rounded inputs:
+    within the dtype's unit roundoff (the 16-bit kernels sum P as rounded for
+    the P @ V product) plus fp32 slack.  A log2 lse, a missing log of the row
+    sum or a dropped bias is off by far more."""
+    B, Sq, Sk, H, Hkv, D, dtype, kw = LSE16_CASES[case]
+    q, k, v = rand((B, Sq, H, D), dtype, 90 + case), rand((B, Sk, Hkv, D), dtype, 95 + case), rand((B, Sk, Hkv, D), dtype, 99)
+    dkw = {key: (val.to(DEV) if torch.is_tensor(val) else val) for key, val in kw.items()}
+    _, lse = triton_attn_func(q, k, v, return_lse=True, **dkw)
+    assert lse.shape == (B, H, Sq) and lse.dtype == torch.float32
+    q64 = q.cpu().double()
+    k64 = k.cpu().double().repeat_interleave(H // Hkv, dim=2)
+    s = torch.einsum("bihd,bjhd->bhij", q64, k64) * kw.get("softmax_scale", D ** -0.5)
+    s = s + torch.from_numpy(orc._bias64(Sq, Sk, H, B, None, kw.get("causal", False), kw.get("window_size"),
+                                         kw.get("alibi_slopes")))
+    ref = torch.logsumexp(s, dim=-1)
+    u = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    err = (lse.cpu().double() - ref).abs().max().item()
+    assert err <= u + 2e-5 * (1 + ref.abs().max().item()), (err, u)
+
+
+@pytest.mark.parametrize("dtype,masked", [(torch.bfloat16, False), (torch.float16, True)])
+def test_outputs_merged_by_lse_equal_one_call(dtype, masked):
+    """Attention over keys [0, Sk) from the calls over [0, c) and [c, Sk)
+    merged by their lse (what a chunked-prefill or ring caller does): as
+    close to the fp64 closed form as the single call, and its lse the
+    log-add-exp of the two."""
+    B, Sq, Sk, H, D, c = 1, 160, 384, 4, 128, 150
+    q, k, v = rand((B, Sq, H, D), dtype, 111), rand((B, Sk, H, D), dtype, 112), rand((B, Sk, H, D), dtype, 113)
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(114)
+        mask = (torch.randn(Sq, Sk, generator=g) * 0.5).masked_fill(torch.rand(Sq, Sk, generator=g) < 0.1, float("-inf"))
+        mask[:, 0] = mask[:, c] = 0.0
+    part = lambda a, b: None if mask is None else mask[:, a:b].to(DEV)
+    o, l = triton_attn_func(q, k, v, attn_mask=part(0, Sk), return_lse=True)
+    o1, l1 = triton_attn_func(q, k[:, :c], v[:, :c], attn_mask=part(0, c), return_lse=True)
+    o2, l2 = triton_attn_func(q, k[:, c:], v[:, c:], attn_mask=part(c, Sk), return_lse=True)
+    l12 = torch.logaddexp(l1.double(), l2.double())
+    w1 = torch.exp(l1.double() - l12).transpose(1, 2)[..., None]
+    w2 = torch.exp(l2.double() - l12).transpose(1, 2)[..., None]
+    merged = (w1 * o1.double() + w2 * o2.double()).cpu()
+    x64 = torch.from_numpy(orc.closed_form(q.cpu(), k.cpu(), v.cpu(), attn_mask=mask))
+    err_one = (o.cpu().double() - x64).abs().max().item()
+    err_merged = (merged - x64).abs().max().item()
+    u = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    assert err_merged <= 2 * err_one + u * x64.abs().max().item(), (err_merged, err_one)
+    assert (l12 - l.double()).abs().max().item() <= 2 * u + 1e-4
+
+
 def test_runs_on_side_stream():
     B, S, H, D = 1, 256, 2, 128
     q, k, v = rand((B, S, H, D), torch.bfloat16, 81), rand((B, S, H, D), torch.bfloat16, 82), rand((B, S, H, D), torch.bfloat16, 83)
