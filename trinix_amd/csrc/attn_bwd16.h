@@ -319,6 +319,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
   struct Item {
     int gh, qt;
   };
+  // Wave 0 loads each item's lse into a register with the item's copies and
+  // writes it to LDS, times log2 e, at the end of the step (before the wait
+  // and barrier that publish the item).  A row with no allowed key has lse
+  // -inf and every score -inf: the finite floor keeps exp2(score - lse2) at 0
+  // instead of exp2(-inf + inf) = NaN.
+  float lse_pend = 0.f;
+  float* lse_dst = nullptr;
+  auto write_lse = [&]() __attribute__((always_inline)) {
+    if (wave == 0 && lse_dst) {
+      *lse_dst = fmaxf(lse_pend * kLog2e, -0.5f * FLT_MAX);
+      lse_dst = nullptr;
+    }
+  };
   auto next_item = [&](Item it) __attribute__((always_inline)) {
     return it.qt + 1 < qt_hi ? Item{it.gh, it.qt + 1} : Item{it.gh + 1, qt_lo};
   };
@@ -328,7 +341,11 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
     load_rows(p.q + b * p.q_sb + hq * p.q_sh, p.q_ss, lds_q + SL * TILE, i0);
     load_rows(p.dout + b * p.do_sb + hq * p.do_sh, p.do_ss, lds_o + SL * TILE, i0);
     const int64_t vo = ((int64_t)b * p.Hq + hq) * p.Sq;
-    if (wave == 0) load_vec(p.lse + vo, lds_l + SL * BQ, i0);
+    if (wave == 0) {
+      // lse of the item's rows, written to LDS times log2 e by write_lse
+      lse_pend = p.lse[vo + i0 + min(lane, p.Sq - 1 - i0)];
+      lse_dst = lds_l + SL * BQ + lane;
+    }
     if (wave == 1) load_vec(p.delta + vo, lds_d + SL * BQ, i0);
     if constexpr (DROP == 2) {
       // keep words of the item's two 32-row blocks and the workgroup's four
@@ -474,11 +491,17 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
         // FMA per element (the distance is exact in fp32 below 2^24, as
         // (float)|i - j| is)
         const float fj = ALIBI ? (float)(j - (i0 + st * 32 + g * 4)) : 0.f;
+        // scale * log2 e * S - lse * log2 e in one FMA per element (lse2: the
+        // LDS copy, already times log2 e and floored)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          x[v] = s[v] * c;
-          if constexpr (ALIBI) x[v] = __builtin_fmaf(fabsf(fj - (float)((v >> 2) * 8 + (v & 3))), slope_l2, x[v]);
+        for (int vq = 0; vq < 4; ++vq) {
+          const f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[vq * 4 + e] = __builtin_fmaf(s[vq * 4 + e], c, -l4[e]);
         }
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if constexpr (ALIBI) x[v] = __builtin_fmaf(fabsf(fj - (float)((v >> 2) * 8 + (v & 3))), slope_l2, x[v]);
         if constexpr (MASK) {
           // rows vq*8 + 4g + 0..3 of the sub-tile: 4 consecutive rows per
           // load group, one dtype switch per group (rows past Sq read row
@@ -502,20 +525,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
             x[v] = qspan.ok(i) ? x[v] : -INFINITY;
           }
         }
-        // Rows with no allowed key have lse -inf and every score -inf; a
-        // finite floor on lse (finite after the scaling) keeps their P at 0
-        // instead of exp2(-inf + inf) = NaN.  Such a row can only sit in a
-        // sub-tile the band cuts or whose mask is read.
-        const bool may_dead = !full || (MASK && mcode > 0);
 #pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-          f32x4_t l4 = *(const f32x4_t*)(l_lds + st * 32 + vq * 8 + g * 4);
-          if (may_dead)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) l4[e] = fmaxf(l4[e], -0.5f * FLT_MAX);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - l4[e] * kLog2e);
-        }
+        for (int v = 0; v < 16; ++v) x[v] = __builtin_amdgcn_exp2f(x[v]);
         u32x4_t pb[2];
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
@@ -598,6 +609,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
     using I1 = std::integral_constant<int, 1>;
     using I2 = std::integral_constant<int, 2>;
     if (n_items > 0) load_item(Item{0, qt_lo}, I0{});
+    write_lse();
     Item ia{0, qt_lo}, ib{0, qt_lo};
     auto step = [&](auto sa_c, auto pa_c, int s) __attribute__((always_inline)) {
       constexpr int SA = decltype(sa_c)::value, PA = decltype(pa_c)::value;
@@ -607,6 +619,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkdv(const BwdParams p) {
       if (s + 1 < n_items) load_item(in, std::integral_constant<int, (SA + 1) % NSL>{});
       if constexpr (!SB) {
         if (s < n_items) stage_a(ia, sa_c, pa_c);
+        write_lse();
       } else {
         if (s > 0) stage_b(ib, std::integral_constant<int, (SA + NSL - 1) % NSL>{}, std::integral_constant<int, 1 - PA>{});
       }
@@ -801,9 +814,10 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
       // per tile: the per-element offsets are immediates, so no per-element
       // value is kept live across tiles
       const float fi = (float)(i - n0 - nb * 32 - 4 * g);
+      // scale * log2 e * S^T - lse * log2 e in one FMA per element
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        x[v] = s[v] * c;
+        x[v] = __builtin_fmaf(s[v], c, -lse2);
         if constexpr (ALIBI) x[v] += slope_l2 * fabsf(fi - (float)((v >> 2) * 8 + (v & 3)));
       }
       if constexpr (MASK) {
@@ -837,7 +851,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             const float dpk = __uint_as_float(__float_as_uint(dp[v]) & keep_word(km, v));
-            z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dpk - dlt);
+            z[v] = __builtin_amdgcn_exp2f(x[v]) * (dpk - dlt);
           }
         } else if constexpr (DROP && ALIBI && MASK && D == 128) {
           // every register in use: each lane makes the call of its own 8-key
@@ -851,7 +865,7 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const float dpk = keep_field(e < 2 ? w0 : w1, e & 1, dkey.thresh) ? dp[vq * 4 + e] : 0.f;
-              z[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e] - lse2) * (dpk - dlt);
+              z[vq * 4 + e] = __builtin_amdgcn_exp2f(x[vq * 4 + e]) * (dpk - dlt);
             }
             __builtin_amdgcn_sched_barrier(0);
           }
@@ -867,12 +881,12 @@ __global__ __launch_bounds__(NW * 64, 2) void attn_bwd_dq(const BwdParams p) {
               for (int e = 0; e < 4; ++e) {
                 const int v = (vp * 2 + h) * 4 + e;
                 const float dpk = keep_field(wq[h][e >> 1], e & 1, dkey.thresh) ? dp[v] : 0.f;
-                z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dpk - dlt);
+                z[v] = __builtin_amdgcn_exp2f(x[v]) * (dpk - dlt);
               }
           }
         } else {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) z[v] = __builtin_amdgcn_exp2f(x[v] - lse2) * (dp[v] - dlt);
+          for (int v = 0; v < 16; ++v) z[v] = __builtin_amdgcn_exp2f(x[v]) * (dp[v] - dlt);
         }
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
