@@ -134,8 +134,15 @@ __device__ inline uint32_t dropout_pair(float (&xa)[4], float (&xb)[4], const Dr
   return bits;
 }
 
-// All ones when bit v of keep bits m is set, else 0 (one v_bfe_i32).
-__device__ inline uint32_t keep_word(uint32_t m, int v) { return (uint32_t)((int)(m << (31 - v)) >> 31); }
+// All ones when bit v of keep bits m is set, else 0: one v_bfe_i32.  The
+// empty asm hides the value from the backend, which would otherwise turn
+// x & keep_word(m, v) into an and, a compare and a select (three
+// instructions per element where v_bfe_i32 and v_and_b32 take two).
+__device__ inline uint32_t keep_word(uint32_t m, int v) {
+  int w = __builtin_amdgcn_sbfe((int)m, v, 1);
+  asm("" : "+v"(w));
+  return (uint32_t)w;
+}
 
 // Combine a value with the one held by lane l ^ 32 (v_permlane32_swap).
 __device__ inline float xlane_max(float x) {
