@@ -94,6 +94,10 @@ def _args(**kw):
     (dict(dtype=7), nat.TRINIX_ERR_BAD_DTYPE),
     (dict(nheads_kv=3), nat.TRINIX_ERR_BAD_SHAPE),
     (dict(seqlen_q=0), nat.TRINIX_ERR_BAD_SHAPE),
+    # every zero-sized dimension is rejected (no empty launch)
+    (dict(seqlen_k=0), nat.TRINIX_ERR_BAD_SHAPE),
+    (dict(batch=0), nat.TRINIX_ERR_BAD_SHAPE),
+    (dict(nheads_q=0), nat.TRINIX_ERR_BAD_SHAPE),
     (dict(q=None), nat.TRINIX_ERR_NULL_POINTER),
     (dict(q_stride=nat.int64x4((1, 1, 1, 2))), nat.TRINIX_ERR_BAD_STRIDE),
     (dict(k_stride=nat.int64x4((8 * 64 * 128, 8 * 128, 130, 1))), nat.TRINIX_ERR_BAD_STRIDE),
@@ -138,6 +142,9 @@ def _bwd_args(**kw):
 @pytest.mark.parametrize("kw,code", [
     (dict(dropout_p=1.0), nat.TRINIX_ERR_BAD_ARGUMENT),
     (dict(lse=None), nat.TRINIX_ERR_NULL_POINTER),
+    (dict(seqlen_q=0), nat.TRINIX_ERR_BAD_SHAPE),
+    (dict(seqlen_k=0), nat.TRINIX_ERR_BAD_SHAPE),
+    (dict(batch=0), nat.TRINIX_ERR_BAD_SHAPE),
     (dict(dropout_keep_map=4096), nat.TRINIX_ERR_BAD_ARGUMENT),  # a keep map without dropout
     (dict(dropout_p=0.1, dropout_keep_map=4100), nat.TRINIX_ERR_BAD_ARGUMENT),
     (dict(dropout_p=0.1, dropout_keep_map=4096, dtype=nat.TRINIX_F32), nat.TRINIX_ERR_BAD_ARGUMENT),

@@ -50,7 +50,8 @@ def triton_attn_func(
         reference's output is detached).
 
     Raises:
-        ValueError: non-GPU tensors or inconsistent shapes.
+        ValueError: non-GPU tensors, inconsistent shapes, or a zero-sized
+            batch, sequence or head dimension (``TRINIX_ERR_BAD_SHAPE``).
         RuntimeError: the HIP kernel library or a gfx950 GPU is unavailable.
     """
     if not q.is_cuda:
