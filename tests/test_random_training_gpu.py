@@ -8,10 +8,11 @@ single keys and decode-shaped calls against long key ranges), q/kv heads
 ALiBi, an additive mask (fp32/bf16/bool, 2-D or 4-D, with -inf entries),
 scale, dropout with and without the keep map, the operands' layout
 (contiguous, (B, H, S, D) transposed, slices of one packed buffer), the lse
-output, and training or inference.  Output, lse and gradients are checked
-against fp64 autograd of the oracle (``functional_attention``, with the
-kernel's Philox keep mask under dropout) next to the same autograd in the
-input dtype ("eager"):
+output, fused RoPE tables (the oracle rotates q and k with the same tables,
+in the input dtype, as eager RoPE does), and training or inference.
+Output, lse and gradients are checked against fp64 autograd of the oracle
+(``functional_attention``, with the kernel's Philox keep mask under
+dropout) next to the same autograd in the input dtype ("eager"):
 
 * output and each gradient: max error within twice eager's plus one unit
   roundoff of the input dtype (fp16: 2e-3, fp32: 1e-5) times the scale
@@ -92,14 +93,28 @@ def draw(seed):
     p = r.choice([0.0, 0.0, 0.0, 0.1, 0.3])
     train = r.random() < (0.7 if Sk < 700 else 0.2) or p > 0
     keep_map = r.choice(["1", "0"])
+    rope_base = r.choice([1e4, 5e5]) if r.random() < 0.2 else None  # fused RoPE (rotary_cos / rotary_sin)
     return dict(B=B, Sq=Sq, Sk=Sk, H=H, Hkv=Hkv, D=D, dtype=dtype, layout=layout, want_lse=want_lse, kw=kw, p=p,
-                train=train, keep_map=keep_map)
+                train=train, keep_map=keep_map, rope_base=rope_base)
+
+
+def _rope_tables(c):
+    """The RoPE tables in the input dtype (the kernel reads them so; the
+    fp64 oracle takes the same rounded values), or None."""
+    if c["rope_base"] is None:
+        return None
+    return orc.rope_tables(max(c["Sq"], c["Sk"]), c["D"], c["rope_base"], c["dtype"])
 
 
 def _oracle(q, k, v, do, dt, c, keep):
     ts = [t.detach().to(dt).clone().requires_grad_(c["train"]) for t in (q, k, v)]
     extra = dict(keep=keep, dropout_p=c["p"]) if c["p"] > 0 else {}
-    out = orc.functional_attention(*ts, **c["kw"], **extra)
+    qa, ka = ts[0], ts[1]
+    tables = _rope_tables(c)
+    if tables is not None:
+        cos, sin = (t.to(dt) for t in tables)
+        qa, ka = orc.apply_rope(qa, cos, sin), orc.apply_rope(ka, cos, sin)
+    out = orc.functional_attention(qa, ka, ts[2], **c["kw"], **extra)
     if not c["train"]:
         return out.detach().double(), []
     out.backward(do.to(dt))
@@ -120,6 +135,9 @@ def _hip(q, k, v, do, c):
             ts = [t.transpose(1, 2).contiguous().transpose(1, 2) for t in ts]
         xs = [t.requires_grad_(train) for t in ts]
     kw = {key: (val.to(DEV) if torch.is_tensor(val) else val) for key, val in c["kw"].items()}
+    tables = _rope_tables(c)
+    if tables is not None:
+        kw["rotary_cos"], kw["rotary_sin"] = (t.to(DEV) for t in tables)
     torch.manual_seed(4321)  # the dropout seed comes from torch's CPU generator
     res = triton_attn_func(*xs, dropout_p=c["p"], return_lse=c["want_lse"], **kw)
     out, lse = res if c["want_lse"] else (res, None)
@@ -167,8 +185,12 @@ def test_random_configuration(seed, monkeypatch):
     fin = torch.isfinite(o64)
     e_max = (do.to(dtype).double().abs() * (o64 - oh).abs()).masked_fill(~fin, 0).sum(-1).max().item()
     cs = abs(kw.get("softmax_scale", D ** -0.5))
-    zero_bound = {"dq": cs * e_max * k.to(dtype).abs().max().item(),
-                  "dk": cs * (H // Hkv) * int(band.sum(0).max()) * e_max * q.to(dtype).abs().max().item()}
+    qx, kx = q.to(dtype), k.to(dtype)  # the operands the scores are taken of (rotated in the input dtype)
+    tables = _rope_tables(c)
+    if tables is not None:
+        qx, kx = orc.apply_rope(qx, *tables), orc.apply_rope(kx, *tables)
+    zero_bound = {"dq": cs * e_max * kx.abs().max().item(),
+                  "dk": cs * (H // Hkv) * int(band.sum(0).max()) * e_max * qx.abs().max().item()}
     for name, h, e, t in [("out", oh, oe, o64)] + list(zip(("dq", "dk", "dv"), gh, ge, g64)):
         f = torch.isfinite(t)
         assert h.shape == t.shape, name
@@ -180,7 +202,7 @@ def test_random_configuration(seed, monkeypatch):
         else:
             assert eh <= 2 * ee + slack * sc, (name, eh, ee, sc)
     if lse is not None:
-        s = torch.einsum("bihd,bjhd->bhij", q.to(dtype).double(), k.to(dtype).double().repeat_interleave(H // Hkv, 2))
+        s = torch.einsum("bihd,bjhd->bhij", qx.double(), kx.double().repeat_interleave(H // Hkv, 2))
         s = s * kw.get("softmax_scale", D ** -0.5) + torch.from_numpy(orc._bias64(
             Sq, Sk, H, B, kw.get("attn_mask"), kw.get("causal", False), kw.get("window_size"), kw.get("alibi_slopes")))
         ref = torch.logsumexp(s, -1)
