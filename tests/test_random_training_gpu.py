@@ -6,10 +6,12 @@ Each seed draws one configuration: batch, lengths (including single rows,
 single keys and decode-shaped calls against long key ranges), q/kv heads
 (MHA, GQA, MQA), head_dim (32, 64, 96, 128, 256), dtype, causal, window,
 ALiBi, an additive mask (fp32/bf16/bool, 2-D or 4-D, with -inf entries),
-scale, dropout with and without the keep map, the operands' layout
-(contiguous, (B, H, S, D) transposed, slices of one packed buffer), the lse
-output, fused RoPE tables (the oracle rotates q and k with the same tables,
-in the input dtype, as eager RoPE does), and training or inference.
+scale, ALiBi slopes per head or per (batch, head), dropout with and
+without the keep map, the operands' layout (contiguous, (B, H, S, D)
+transposed, head slices of one packed buffer, last-dim slices of one fused
+projection output), the lse output, fused RoPE tables (the oracle rotates
+q and k with the same tables, in the input dtype, as eager RoPE does), and
+training or inference.
 Output, lse and gradients are checked against fp64 autograd of the oracle
 (``functional_attention``, with the kernel's Philox keep mask under
 dropout) next to the same autograd in the input dtype ("eager"):
@@ -94,6 +96,15 @@ def draw(seed):
     train = r.random() < (0.7 if Sk < 700 else 0.2) or p > 0
     keep_map = r.choice(["1", "0"])
     rope_base = r.choice([1e4, 5e5]) if r.random() < 0.2 else None  # fused RoPE (rotary_cos / rotary_sin)
+    # ALiBi slopes as (H,), (1, H) or (B, H) (per-batch slopes)
+    slope_shape = r.choice(["h", "1h", "bh"])
+    if "alibi_slopes" in kw and slope_shape != "h":
+        sl = kw["alibi_slopes"]
+        kw["alibi_slopes"] = (sl[None] if slope_shape == "1h" else
+                              torch.stack([sl * (1.0 + 0.5 * bb) for bb in range(B)]))
+    # q, k, v as last-dim slices of one fused projection output (B, S, H, 3D + 8)
+    if r.random() < 0.15 and H == Hkv and Sq == Sk and layout == "bshd":
+        layout = "qkv_last"
     return dict(B=B, Sq=Sq, Sk=Sk, H=H, Hkv=Hkv, D=D, dtype=dtype, layout=layout, want_lse=want_lse, kw=kw, p=p,
                 train=train, keep_map=keep_map, rope_base=rope_base)
 
@@ -125,7 +136,12 @@ def _hip(q, k, v, do, c):
     B, Sq, Sk, H, Hkv, D, dtype = (c[n] for n in ("B", "Sq", "Sk", "H", "Hkv", "D", "dtype"))
     train = c["train"]
     ts = [t.to(DEV, dtype) for t in (q, k, v)]
-    if c["layout"] == "packed":  # one (B, S, H + 2 Hkv + 1, D) buffer, the extra head pads the row stride
+    if c["layout"] == "qkv_last":  # one (B, S, H, 3D + 8) buffer, q / k / v side by side in the last dim
+        buf = torch.zeros(B, Sq, H, 3 * D + 8, device=DEV, dtype=dtype)
+        buf[..., :D], buf[..., D:2 * D], buf[..., 2 * D:3 * D] = ts
+        buf.requires_grad_(train)
+        xs = [buf[..., :D], buf[..., D:2 * D], buf[..., 2 * D:3 * D]]
+    elif c["layout"] == "packed":  # one (B, S, H + 2 Hkv + 1, D) buffer, the extra head pads the row stride
         buf = torch.zeros(B, max(Sq, Sk), H + 2 * Hkv + 1, D, device=DEV, dtype=dtype)
         buf[:, :Sq, :H], buf[:, :Sk, H:H + Hkv], buf[:, :Sk, H + Hkv:H + 2 * Hkv] = ts
         buf.requires_grad_(train)
@@ -147,6 +163,9 @@ def _hip(q, k, v, do, c):
         if c["layout"] == "packed":
             gb = buf.grad
             grads = [gb[:, :Sq, :H], gb[:, :Sk, H:H + Hkv], gb[:, :Sk, H + Hkv:H + 2 * Hkv]]
+        elif c["layout"] == "qkv_last":
+            gb = buf.grad
+            grads = [gb[..., :D], gb[..., D:2 * D], gb[..., 2 * D:3 * D]]
         else:
             grads = [t.grad for t in xs]
     return (out.detach().cpu().double(), [g.cpu().double() for g in grads],
